@@ -1,0 +1,714 @@
+// The C ABI of include/beatlm_hip.h: context, arenas and kernels.
+//
+// bl_kernels_create is the HIP counterpart of the reference's Kernels::new
+// (crates/beatlm/src/codegen/kernels.rs:63-184): it checks every spec once,
+// resolves each binding set's bindings to device addresses inside the
+// arenas, picks the kernel variant and launch shape, and allocates the
+// scratch any kernel needs, so that bl_kernels_encode (Kernels::encode,
+// :217-233) is a launch over prepared arguments and nothing else.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "spec.hpp"
+#include "timer.hpp"
+
+using namespace bl;
+
+struct bl_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string error;
+    uint64_t allocations = 0;
+    uint32_t f32_math = BL_F32_MATH_SPLIT_BF16;
+    uint32_t compute_units = 0;
+    uint32_t wall_clock_khz = 0;
+    bl_device_profile_t profile{};
+};
+
+namespace {
+
+int fail(bl_ctx *ctx, int code, const char *fmt, ...) {
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        ctx->error = buf;
+    }
+    return code;
+}
+
+int hip_fail(bl_ctx *ctx, hipError_t e, const char *what) {
+    return fail(ctx, BL_ERR_HIP, "%s: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+// The placement alignment every plan made for this backend uses: HBM
+// transactions are 128-byte lines and the kernels' 16-byte vector loads need
+// 16; 256 matches the reference's baseline (device.rs:97-113), so a baseline
+// plan is valid here unchanged.
+constexpr uint32_t PLACEMENT_ALIGNMENT = 256;
+
+}  // namespace
+
+struct bl_arenas {
+    bl_ctx *ctx = nullptr;
+    char *base = nullptr;
+    std::vector<uint64_t> offset, size;
+    uint64_t total = 0;
+};
+
+// ---- context ----
+
+extern "C" uint32_t bl_abi_version(void) { return BL_ABI_VERSION; }
+
+extern "C" int bl_ctx_create(int device_ordinal, bl_ctx **out) {
+    if (!out) return BL_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return BL_ERR_HIP;
+    if (device_ordinal < 0 || device_ordinal >= count) return BL_ERR_INVALID_ARGUMENT;
+    bl_ctx *ctx = new bl_ctx();
+    ctx->device = device_ordinal;
+    if ((e = hipSetDevice(device_ordinal)) != hipSuccess) { delete ctx; return BL_ERR_HIP; }
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device_ordinal)) != hipSuccess) { delete ctx; return BL_ERR_HIP; }
+    // One stream at the default priority; the frame loop's work is ordered on it.
+    if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete ctx;
+        return BL_ERR_HIP;
+    }
+    int khz = 0;
+    hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_ordinal);
+    ctx->wall_clock_khz = (uint32_t)khz;
+    ctx->compute_units = (uint32_t)prop.multiProcessorCount;
+    bl_device_profile_t &p = ctx->profile;
+    // A hipMalloc'd arena is addressed by 64-bit pointers: no binding limit
+    // below the device's memory (kernels index elements with 32-bit rows and
+    // 64-bit offsets).
+    p.max_storage_buffer_binding_size = prop.totalGlobalMem;
+    p.max_buffer_size = prop.totalGlobalMem;
+    p.min_storage_buffer_offset_alignment = PLACEMENT_ALIGNMENT;
+    p.max_compute_workgroup_storage_size = (uint32_t)prop.sharedMemPerBlock;
+    p.max_compute_invocations_per_workgroup = (uint32_t)prop.maxThreadsPerBlock;
+    p.max_compute_workgroup_size[0] = (uint32_t)prop.maxThreadsDim[0];
+    p.max_compute_workgroup_size[1] = (uint32_t)prop.maxThreadsDim[1];
+    p.max_compute_workgroup_size[2] = (uint32_t)prop.maxThreadsDim[2];
+    p.max_compute_workgroups_per_dimension = (uint32_t)std::min<int>(prop.maxGridSize[1], prop.maxGridSize[2]);
+    p.max_storage_buffers_per_shader_stage = BL_MAX_BINDINGS;
+    p.shader_f16 = 1;
+    p.subgroups = 1;
+    p.timestamp_query = 1;
+    p.compute_units = ctx->compute_units;
+    p.wave_size = (uint32_t)prop.warpSize;
+    p.total_memory = prop.totalGlobalMem;
+    snprintf(p.name, sizeof p.name, "%s", prop.name);
+    snprintf(p.arch, sizeof p.arch, "%s", prop.gcnArchName);
+    *out = ctx;
+    return BL_OK;
+}
+
+extern "C" void bl_ctx_destroy(bl_ctx *ctx) {
+    if (!ctx) return;
+    hipSetDevice(ctx->device);
+    if (ctx->stream) {
+        hipStreamSynchronize(ctx->stream);
+        hipStreamDestroy(ctx->stream);
+    }
+    delete ctx;
+}
+
+extern "C" const char *bl_last_error(const bl_ctx *ctx) { return ctx ? ctx->error.c_str() : "no context"; }
+
+extern "C" int bl_device_profile(bl_ctx *ctx, bl_device_profile_t *out) {
+    if (!ctx || !out) return BL_ERR_INVALID_ARGUMENT;
+    *out = ctx->profile;
+    return BL_OK;
+}
+
+extern "C" int bl_ctx_set_f32_math(bl_ctx *ctx, uint32_t mode) {
+    if (!ctx) return BL_ERR_INVALID_ARGUMENT;
+    if (mode != BL_F32_MATH_SPLIT_BF16 && mode != BL_F32_MATH_MFMA_F32)
+        return fail(ctx, BL_ERR_INVALID_ARGUMENT, "unknown f32 math mode %u", mode);
+    ctx->f32_math = mode;
+    return BL_OK;
+}
+
+extern "C" int bl_ctx_synchronize(bl_ctx *ctx) {
+    if (!ctx) return BL_ERR_INVALID_ARGUMENT;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? BL_OK : hip_fail(ctx, e, "hipStreamSynchronize");
+}
+
+extern "C" uint64_t bl_ctx_allocations(const bl_ctx *ctx) { return ctx ? ctx->allocations : 0; }
+
+extern "C" void *bl_ctx_stream(bl_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+// Device memory the backend owns, counted so a host can check the frame loop
+// allocates nothing.
+void *bl_device_alloc(bl_ctx *ctx, uint64_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    ctx->allocations++;
+    return p;
+}
+
+bool bl_events_counted(bl_ctx *ctx, uint64_t n) {
+    ctx->allocations += n;
+    return true;
+}
+
+hipStream_t bl_stream_of(bl_ctx *ctx) { return ctx->stream; }
+int bl_fail(bl_ctx *ctx, int code, const char *msg) { return fail(ctx, code, "%s", msg); }
+
+// ---- arenas ----
+
+extern "C" int bl_arenas_create(bl_ctx *ctx, const uint64_t *sizes, uint32_t n, bl_arenas **out) {
+    if (!ctx || !out || (n && !sizes)) return BL_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    hipSetDevice(ctx->device);
+    bl_arenas *a = new bl_arenas();
+    a->ctx = ctx;
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (sizes[i] > ctx->profile.max_buffer_size) {
+            delete a;
+            return fail(ctx, BL_ERR_PLAN_NOT_VALID_ON_DEVICE,
+                        "arena %u of %llu bytes exceeds the device's %llu", i,
+                        (unsigned long long)sizes[i], (unsigned long long)ctx->profile.max_buffer_size);
+        }
+        total = (total + PLACEMENT_ALIGNMENT - 1) / PLACEMENT_ALIGNMENT * PLACEMENT_ALIGNMENT;
+        a->offset.push_back(total);
+        a->size.push_back(sizes[i]);
+        total += sizes[i];
+    }
+    a->total = total;
+    if (total) {
+        // One allocation for every arena of the plan.
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, total);
+        if (e != hipSuccess) {
+            delete a;
+            return hip_fail(ctx, e, "hipMalloc of the arenas");
+        }
+        ctx->allocations++;
+        a->base = (char *)p;
+    }
+    *out = a;
+    return BL_OK;
+}
+
+extern "C" void bl_arenas_destroy(bl_arenas *a) {
+    if (!a) return;
+    if (a->base) {
+        hipSetDevice(a->ctx->device);
+        hipStreamSynchronize(a->ctx->stream);
+        hipFree(a->base);
+    }
+    delete a;
+}
+
+static int check_range(bl_arenas *a, uint32_t arena, uint64_t offset, uint64_t bytes) {
+    if (arena >= a->size.size())
+        return fail(a->ctx, BL_ERR_UNKNOWN_ARENA, "arena %u does not exist in this set", arena);
+    if (offset > a->size[arena] || bytes > a->size[arena] - offset)
+        return fail(a->ctx, BL_ERR_PLACEMENT_OUT_OF_RANGE,
+                    "placement at offset %llu of %llu bytes does not lie inside arena %u",
+                    (unsigned long long)offset, (unsigned long long)bytes, arena);
+    return BL_OK;
+}
+
+extern "C" int bl_arenas_write(bl_arenas *a, uint32_t arena, uint64_t offset, const void *src, uint64_t bytes) {
+    if (!a || (bytes && !src)) return BL_ERR_INVALID_ARGUMENT;
+    if (int r = check_range(a, arena, offset, bytes)) return r;
+    if (!bytes) return BL_OK;
+    hipSetDevice(a->ctx->device);
+    hipError_t e = hipMemcpyAsync(a->base + a->offset[arena] + offset, src, bytes, hipMemcpyHostToDevice,
+                                  a->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(a->ctx->stream);
+    return e == hipSuccess ? BL_OK : hip_fail(a->ctx, e, "arena write");
+}
+
+extern "C" int bl_arenas_read(bl_arenas *a, uint32_t arena, uint64_t offset, void *dst, uint64_t bytes) {
+    if (!a || (bytes && !dst)) return BL_ERR_INVALID_ARGUMENT;
+    if (int r = check_range(a, arena, offset, bytes)) return r;
+    if (!bytes) return BL_OK;
+    hipSetDevice(a->ctx->device);
+    hipError_t e = hipMemcpyAsync(dst, a->base + a->offset[arena] + offset, bytes, hipMemcpyDeviceToHost,
+                                  a->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(a->ctx->stream);
+    return e == hipSuccess ? BL_OK : hip_fail(a->ctx, e, "arena read");
+}
+
+extern "C" int bl_arenas_device_ptr(bl_arenas *a, uint32_t arena, uint64_t offset, void **out) {
+    if (!a || !out) return BL_ERR_INVALID_ARGUMENT;
+    if (int r = check_range(a, arena, offset, 0)) return r;
+    *out = a->base + a->offset[arena] + offset;
+    return BL_OK;
+}
+
+// ---- kernels ----
+
+namespace {
+
+enum class Family { LAYER_NORM, GEMM, GATHER, SOFTMAX, FLASH, ELEMENT };
+
+struct Launch {
+    Family family;
+    Math math = Math::F32;
+    int tile = 0;
+    bool f16 = false;
+    Gather gather = Gather::SCORES;
+    PerElement element = PerElement::MAP;
+    LayerNormArgs ln;
+    GemmArgs gemm;
+    GatherArgs ga;
+    SoftmaxArgs sm;
+    FlashArgs fl;
+    ElementArgs el;
+};
+
+struct Kernel {
+    std::string label;
+    std::vector<Launch> per_set;
+};
+
+const char *main_name(uint32_t m) {
+    switch (m) {
+    case BL_MAIN_LAYER_NORM: return "layernorm";
+    case BL_MAIN_MATMUL: return "matmul";
+    case BL_MAIN_ATTENTION_SCORES: return "attention_scores";
+    case BL_MAIN_SOFTMAX: return "softmax";
+    case BL_MAIN_ATTENTION_VALUES: return "attention_values";
+    case BL_MAIN_PATCH_EMBED: return "patch_embed";
+    case BL_MAIN_PREPEND_TOKEN: return "prepend_token";
+    case BL_MAIN_TOKENS_TO_MAP: return "tokens_to_map";
+    case BL_MAIN_MAP: return "map";
+    case BL_MAIN_FLASH_ATTENTION: return "flash_attention";
+    default: return nullptr;
+    }
+}
+
+const char *epi_name(uint32_t k) {
+    switch (k) {
+    case BL_EPI_ADD: return "add";
+    case BL_EPI_RELU: return "relu";
+    case BL_EPI_GELU: return "gelu";
+    case BL_EPI_GELU_ERF: return "gelu_erf";
+    case BL_EPI_SCALE: return "scale";
+    case BL_EPI_CHANNEL_SCALE: return "channel_scale";
+    default: return nullptr;
+    }
+}
+
+uint64_t mul(std::initializer_list<uint64_t> v) {
+    uint64_t r = 1;
+    for (uint64_t x : v) r *= x;
+    return r;
+}
+
+// What a spec's main operation reads and writes, in elements; its split
+// extent and grain (MainOp::split_extent / split_grain, kernel.rs:1521-1543).
+struct Shape {
+    std::vector<uint64_t> reads;
+    uint64_t out = 0;
+    uint32_t extent = 0;
+    uint32_t grain = 1;
+    uint64_t per_unit = 1;  // output elements per unit of the split dimension
+};
+
+bool shape_of(const bl_spec &s, Shape &sh, std::string &why) {
+    const uint32_t *d = s.dims;
+    switch (s.main) {
+    case BL_MAIN_LAYER_NORM:
+        sh.reads = {mul({d[0], d[1]}), d[1], d[1]};
+        sh.out = mul({d[0], d[1]});
+        sh.extent = d[0];
+        sh.per_unit = d[1];
+        if (!(s.epsilon > 0.0f && s.epsilon < 1e30f)) { why = "layer norm epsilon is not finite and positive"; return false; }
+        return d[0] && d[1];
+    case BL_MAIN_MATMUL:
+        sh.reads = {mul({d[0], d[1]}), mul({d[1], d[2]})};
+        if (d[3]) sh.reads.push_back(d[2]);
+        sh.out = mul({d[0], d[2]});
+        sh.extent = d[0];
+        sh.grain = 64;
+        sh.per_unit = d[2];
+        return d[0] && d[1] && d[2];
+    case BL_MAIN_ATTENTION_SCORES:
+        sh.reads = {mul({d[0], 3, d[1], d[2]})};
+        sh.out = mul({d[0], d[1], d[0]});
+        sh.extent = d[0];
+        sh.grain = 64;
+        sh.per_unit = mul({d[1], d[0]});
+        return d[0] && d[1] && d[2];
+    case BL_MAIN_SOFTMAX:
+        sh.reads = {mul({d[0], d[1]})};
+        sh.out = mul({d[0], d[1]});
+        sh.extent = d[0];
+        sh.per_unit = d[1];
+        return d[0] && d[1];
+    case BL_MAIN_ATTENTION_VALUES:
+        sh.reads = {mul({d[0], d[1], d[0]}), mul({d[0], 3, d[1], d[2]})};
+        sh.out = mul({d[0], d[1], d[2]});
+        sh.extent = d[0];
+        sh.grain = 64;
+        sh.per_unit = mul({d[1], d[2]});
+        return d[0] && d[1] && d[2];
+    case BL_MAIN_PATCH_EMBED:
+        sh.reads = {mul({d[0], d[2], d[1], d[2], d[3]}), mul({d[2], d[2], d[3], d[4]})};
+        if (d[5]) sh.reads.push_back(d[4]);
+        sh.out = mul({d[0], d[1], d[4]});
+        sh.extent = d[0] * d[1];
+        sh.grain = 64;
+        sh.per_unit = d[4];
+        return d[0] && d[1] && d[2] && d[3] && d[4];
+    case BL_MAIN_PREPEND_TOKEN:
+        sh.reads = {d[1], mul({d[0], d[1]})};
+        sh.out = mul({(uint64_t)d[0] + 1, d[1]});
+        sh.extent = (uint32_t)sh.out;
+        return d[0] && d[1];
+    case BL_MAIN_TOKENS_TO_MAP:
+        sh.reads = {(mul({d[0], d[1]}) + 1) * d[2]};
+        sh.out = mul({d[0], d[1], d[2]});
+        sh.extent = (uint32_t)sh.out;
+        return d[0] && d[1] && d[2];
+    case BL_MAIN_MAP:
+        sh.reads = {d[0]};
+        sh.out = d[0];
+        sh.extent = d[0];
+        return d[0] != 0;
+    case BL_MAIN_FLASH_ATTENTION:
+        sh.reads = {mul({d[0], 3, d[1], d[2]})};
+        sh.out = mul({d[0], d[1], d[2]});
+        sh.extent = d[0];
+        sh.grain = 64;
+        sh.per_unit = mul({d[1], d[2]});
+        if (d[2] != FLASH_HEAD_DIM) { why = "the flash kernel needs a head width of 64"; return false; }
+        if (!(s.scale == s.scale) || s.scale == INFINITY || s.scale == -INFINITY) { why = "non-finite scale"; return false; }
+        return d[0] && d[1];
+    default:
+        why = "unknown main operation";
+        return false;
+    }
+}
+
+uint64_t round4(uint64_t bytes) { return (bytes + 3) / 4 * 4; }
+
+}  // namespace
+
+struct bl_kernels {
+    bl_ctx *ctx = nullptr;
+    bl_arenas *arenas = nullptr;
+    std::vector<Kernel> kernels;
+    uint32_t sets = 1;
+    void *scratch = nullptr;
+};
+
+extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs, uint32_t n,
+                                 const bl_binding_set *sets, uint32_t n_sets, bl_kernels **out) {
+    if (!ctx || !arenas || !out || (n && !specs) || (n_sets && !sets)) return BL_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    hipSetDevice(ctx->device);
+    const bl_binding_set identity{nullptr, 0};
+    if (n_sets == 0) {
+        sets = &identity;
+        n_sets = 1;
+    }
+    auto *ks = new bl_kernels();
+    ks->ctx = ctx;
+    ks->arenas = arenas;
+    ks->sets = n_sets;
+    uint64_t scratch_bytes = 0;
+    std::vector<std::pair<size_t, size_t>> flash_users;  // (kernel, set) whose FlashArgs need scratch
+
+    auto bad = [&](int code, const char *fmt, auto... args) {
+        delete ks;
+        return fail(ctx, code, fmt, args...);
+    };
+
+    for (uint32_t ki = 0; ki < n; ki++) {
+        const bl_spec &s = specs[ki];
+        const char *mname = main_name(s.main);
+        if (!mname) return bad(BL_ERR_KERNEL, "kernel %u: unknown main operation %u", ki, s.main);
+        std::string name = mname;
+        for (uint32_t e = 0; e < s.n_epilogue && e < BL_MAX_EPILOGUE; e++) {
+            const char *en = epi_name(s.epilogue[e].kind);
+            if (!en) return bad(BL_ERR_KERNEL, "kernel %u: unknown epilogue step %u", ki, s.epilogue[e].kind);
+            name += "+";
+            name += en;
+        }
+        Shape sh;
+        std::string why;
+        if (!shape_of(s, sh, why))
+            return bad(BL_ERR_KERNEL, "kernel %s: %s", name.c_str(), why.empty() ? "a zero dimension" : why.c_str());
+        if (s.n_bindings < 2 || s.n_bindings > BL_MAX_BINDINGS || s.n_epilogue > BL_MAX_EPILOGUE)
+            return bad(BL_ERR_KERNEL, "kernel %s: %u bindings", name.c_str(), s.n_bindings);
+        if (s.n_reads != sh.reads.size())
+            return bad(BL_ERR_KERNEL, "kernel %s: main operation reads %zu tensors, spec names %u", name.c_str(),
+                       sh.reads.size(), s.n_reads);
+        const uint32_t dtype = s.bindings[0].dtype;
+        if (dtype != BL_F32 && dtype != BL_F16) return bad(BL_ERR_KERNEL, "kernel %s: unknown dtype", name.c_str());
+        const uint64_t esz = dtype == BL_F16 ? 2 : 4;
+        for (uint32_t b = 0; b < s.n_bindings; b++)
+            if (s.bindings[b].dtype != dtype)
+                return bad(BL_ERR_KERNEL, "kernel %s: bindings of mixed element types", name.c_str());
+        // Every binding's placement holds what the operation's shape says.
+        std::vector<uint64_t> need(s.n_bindings, 0);
+        for (uint32_t r = 0; r < s.n_reads; r++) {
+            if (s.reads[r] >= s.n_bindings - 1)
+                return bad(BL_ERR_KERNEL, "kernel %s: read %u names binding %u", name.c_str(), r, s.reads[r]);
+            need[s.reads[r]] = round4(sh.reads[r] * esz);
+        }
+        need[s.n_bindings - 1] = round4(sh.out * esz);
+        for (uint32_t e = 0; e < s.n_epilogue; e++) {
+            const bl_epilogue &ep = s.epilogue[e];
+            if (ep.kind == BL_EPI_ADD || ep.kind == BL_EPI_CHANNEL_SCALE) {
+                if (ep.operand >= s.n_bindings - 1)
+                    return bad(BL_ERR_KERNEL, "kernel %s: epilogue step %u names binding %u", name.c_str(), e,
+                               ep.operand);
+                uint64_t el = sh.out;
+                if (ep.kind == BL_EPI_CHANNEL_SCALE) {
+                    if (!ep.channels || sh.out % ep.channels)
+                        return bad(BL_ERR_KERNEL, "kernel %s: channel scale of %u channels", name.c_str(), ep.channels);
+                    el = ep.channels;
+                }
+                need[ep.operand] = round4(el * esz);
+            }
+        }
+        for (uint32_t b = 0; b < s.n_bindings; b++)
+            if (need[b] == 0 || s.bindings[b].size != need[b])
+                return bad(BL_ERR_KERNEL, "kernel %s: binding %u (tensor %u) is %llu bytes, the shape needs %llu",
+                           name.c_str(), b, s.bindings[b].tensor, (unsigned long long)s.bindings[b].size,
+                           (unsigned long long)need[b]);
+        // The part: a non-empty range of the split dimension, starting on the grain.
+        const bl_part &pt = s.part;
+        if (pt.count == 0 || pt.index >= pt.count || pt.start >= pt.end || pt.end > sh.extent ||
+            pt.start % sh.grain != 0)
+            return bad(BL_ERR_KERNEL, "kernel %s: part %u/%u covers %u..%u of %u (grain %u)", name.c_str(),
+                       pt.index + 1, pt.count, pt.start, pt.end, sh.extent, sh.grain);
+
+        Kernel k;
+        k.label = name;
+        if (pt.count > 1) k.label += " part " + std::to_string(pt.index + 1) + "/" + std::to_string(pt.count);
+
+        for (uint32_t si = 0; si < n_sets; si++) {
+            // Resolve every binding of this set to a device address.
+            void *ptr[BL_MAX_BINDINGS];
+            for (uint32_t b = 0; b < s.n_bindings; b++) {
+                bl_binding bd = s.bindings[b];
+                for (uint32_t t = 0; t < sets[si].count; t++) {
+                    const bl_substitution &sub = sets[si].items[t];
+                    if (sub.original == bd.tensor) {
+                        if (sub.size != bd.size)
+                            return bad(BL_ERR_STAND_IN_SIZE,
+                                       "tensor %u stands in for tensor %u but its placement is %llu bytes, not %llu",
+                                       sub.stand_in, sub.original, (unsigned long long)sub.size,
+                                       (unsigned long long)bd.size);
+                        bd.arena = sub.arena;
+                        bd.offset = sub.offset;
+                    }
+                }
+                if (bd.arena >= arenas->size.size())
+                    return bad(BL_ERR_UNKNOWN_ARENA, "arena %u does not exist in this set", bd.arena);
+                if (bd.offset > arenas->size[bd.arena] || bd.size > arenas->size[bd.arena] - bd.offset)
+                    return bad(BL_ERR_PLACEMENT_OUT_OF_RANGE,
+                               "placement at offset %llu of %llu bytes does not lie inside its arena",
+                               (unsigned long long)bd.offset, (unsigned long long)bd.size);
+                if (bd.offset % PLACEMENT_ALIGNMENT)
+                    return bad(BL_ERR_MISALIGNED_PLACEMENT, "placement at offset %llu is not aligned to %u bytes",
+                               (unsigned long long)bd.offset, PLACEMENT_ALIGNMENT);
+                ptr[b] = arenas->base + arenas->offset[bd.arena] + bd.offset;
+            }
+            EpilogueArgs epi{};
+            epi.n = (int)s.n_epilogue;
+            for (uint32_t e = 0; e < s.n_epilogue; e++) {
+                epi.kind[e] = (int)s.epilogue[e].kind;
+                epi.factor[e] = s.epilogue[e].factor;
+                epi.channels[e] = s.epilogue[e].channels;
+                epi.operand[e] = (s.epilogue[e].kind == BL_EPI_ADD || s.epilogue[e].kind == BL_EPI_CHANNEL_SCALE)
+                                     ? ptr[s.epilogue[e].operand]
+                                     : nullptr;
+            }
+            void *out_ptr = ptr[s.n_bindings - 1];
+            auto rd = [&](int i) -> const void * { return ptr[s.reads[i]]; };
+            const bool f16 = dtype == BL_F16;
+            const Math fmath = f16 ? Math::F16 : (ctx->f32_math == BL_F32_MATH_MFMA_F32 ? Math::F32 : Math::SPLIT);
+            const uint32_t *d = s.dims;
+            Launch L{};
+            L.f16 = f16;
+            L.math = fmath;
+            std::string variant;
+            switch (s.main) {
+            case BL_MAIN_LAYER_NORM:
+                L.family = Family::LAYER_NORM;
+                L.ln = LayerNormArgs{rd(0), rd(1), rd(2), out_ptr, d[0], d[1], pt.start, pt.end, s.epsilon, epi};
+                variant = "wave-per-row";
+                break;
+            case BL_MAIN_MATMUL: {
+                L.family = Family::GEMM;
+                L.gemm = GemmArgs{rd(0), rd(1), d[3] ? rd(2) : nullptr, out_ptr, d[0], d[2], d[1], pt.start, pt.end, epi};
+                // The largest tile that still gives every CU a workgroup.
+                const uint32_t rows = pt.end - pt.start;
+                const int order[] = {TILE_128x128, TILE_64x128, TILE_128x64, TILE_64x64, TILE_32x64};
+                int chosen = TILE_32x64;
+                for (int t : order) {
+                    uint64_t wgs = (uint64_t)((rows + gemm_tile_rows(t) - 1) / gemm_tile_rows(t)) *
+                                   ((d[2] + gemm_tile_cols(t) - 1) / gemm_tile_cols(t));
+                    if (wgs >= ctx->compute_units) { chosen = t; break; }
+                }
+                L.tile = chosen;
+                variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
+                          " " + std::to_string(gemm_tile_rows(chosen)) + "x" + std::to_string(gemm_tile_cols(chosen));
+                break;
+            }
+            case BL_MAIN_ATTENTION_SCORES:
+                L.family = Family::GATHER;
+                L.gather = Gather::SCORES;
+                L.ga = GatherArgs{rd(0), rd(0), nullptr, out_ptr, d[0], d[2], d[1], pt.start, pt.end, d[0], d[1], d[2], 0, epi};
+                variant = "valu-tiled";
+                break;
+            case BL_MAIN_ATTENTION_VALUES:
+                L.family = Family::GATHER;
+                L.gather = Gather::VALUES;
+                L.ga = GatherArgs{rd(0), rd(1), nullptr, out_ptr, d[2], d[0], d[1], pt.start, pt.end, d[0], d[1], d[2], 0, epi};
+                variant = "valu-tiled";
+                break;
+            case BL_MAIN_PATCH_EMBED:
+                L.family = Family::GATHER;
+                L.gather = Gather::PATCH;
+                L.ga = GatherArgs{rd(0), rd(1), d[5] ? rd(2) : nullptr, out_ptr, d[4], d[2] * d[2] * d[3], 1,
+                                  pt.start, pt.end, d[1], d[2], d[3], d[1] * d[2], epi};
+                variant = "valu-tiled";
+                break;
+            case BL_MAIN_SOFTMAX:
+                L.family = Family::SOFTMAX;
+                L.sm = SoftmaxArgs{rd(0), out_ptr, d[1], pt.start, pt.end, epi};
+                variant = "workgroup-per-row";
+                break;
+            case BL_MAIN_PREPEND_TOKEN:
+                L.family = Family::ELEMENT;
+                L.element = PerElement::PREPEND;
+                L.el = ElementArgs{rd(0), rd(1), out_ptr, pt.start, pt.end, d[1], epi};
+                variant = "per-element";
+                break;
+            case BL_MAIN_TOKENS_TO_MAP:
+                L.family = Family::ELEMENT;
+                L.element = PerElement::DROP_FIRST;
+                L.el = ElementArgs{rd(0), nullptr, out_ptr, pt.start, pt.end, d[2], epi};
+                variant = "per-element";
+                break;
+            case BL_MAIN_MAP:
+                L.family = Family::ELEMENT;
+                L.element = PerElement::MAP;
+                L.el = ElementArgs{rd(0), nullptr, out_ptr, pt.start, pt.end, 0, epi};
+                variant = "per-element";
+                break;
+            case BL_MAIN_FLASH_ATTENTION: {
+                if (s.n_epilogue) return bad(BL_ERR_KERNEL, "kernel %s: the flash kernel takes no epilogue", name.c_str());
+                L.family = Family::FLASH;
+                const uint32_t rows = pt.end - pt.start;
+                const uint32_t wgs = (rows + FLASH_ROWS - 1) / FLASH_ROWS * d[1];
+                const uint32_t ntiles = (d[0] + 63) / 64;
+                // Enough workgroups for two per CU, each split keeping two key tiles or more.
+                uint32_t splits = (2 * ctx->compute_units + wgs - 1) / wgs;
+                splits = std::max<uint32_t>(1, std::min<uint32_t>(splits, ntiles / 2));
+                L.fl = FlashArgs{rd(0), out_ptr, nullptr, nullptr, d[0], d[1], pt.start, pt.end, splits, s.scale};
+                if (splits > 1) {
+                    uint64_t need_bytes = (uint64_t)splits * d[0] * d[1] * (FLASH_HEAD_DIM + 2) * sizeof(float);
+                    scratch_bytes = std::max(scratch_bytes, need_bytes);
+                    flash_users.push_back({ki, si});
+                }
+                variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
+                          " splits=" + std::to_string(splits);
+                break;
+            }
+            }
+            if (si == 0) k.label += " @ " + variant;
+            k.per_set.push_back(L);
+        }
+        ks->kernels.push_back(std::move(k));
+    }
+    if (scratch_bytes) {
+        ks->scratch = bl_device_alloc(ctx, scratch_bytes);
+        if (!ks->scratch) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
+        for (auto [ki, si] : flash_users) {
+            FlashArgs &f = ks->kernels[ki].per_set[si].fl;
+            f.partial = (float *)ks->scratch;
+            f.stats = (float *)ks->scratch + (uint64_t)f.splits * f.tokens * f.heads * FLASH_HEAD_DIM;
+        }
+    }
+    *out = ks;
+    return BL_OK;
+}
+
+extern "C" void bl_kernels_destroy(bl_kernels *k) {
+    if (!k) return;
+    if (k->scratch) {
+        hipSetDevice(k->ctx->device);
+        hipStreamSynchronize(k->ctx->stream);
+        hipFree(k->scratch);
+    }
+    delete k;
+}
+
+extern "C" uint32_t bl_kernels_len(const bl_kernels *k) { return k ? (uint32_t)k->kernels.size() : 0; }
+extern "C" uint32_t bl_kernels_sets(const bl_kernels *k) { return k ? k->sets : 0; }
+extern "C" const char *bl_kernels_label(const bl_kernels *k, uint32_t i) {
+    return (k && i < k->kernels.size()) ? k->kernels[i].label.c_str() : nullptr;
+}
+
+static hipError_t launch(const Launch &L, hipStream_t s) {
+    switch (L.family) {
+    case Family::LAYER_NORM: return launch_layernorm(L.ln, L.f16, s);
+    case Family::GEMM: return launch_gemm(L.gemm, L.math, L.tile, s);
+    case Family::GATHER: return launch_gather(L.ga, L.gather, L.f16, s);
+    case Family::SOFTMAX: return launch_softmax(L.sm, L.f16, s);
+    case Family::FLASH: return launch_flash(L.fl, L.math, s);
+    case Family::ELEMENT: return launch_element(L.el, L.element, L.f16, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, bl_timer *timer, uint32_t tag) {
+    if (!k) return BL_ERR_INVALID_ARGUMENT;
+    if (kernel >= k->kernels.size()) return fail(k->ctx, BL_ERR_NO_SUCH_KERNEL, "there is no kernel %u", kernel);
+    if (set >= k->sets) return fail(k->ctx, BL_ERR_NO_SUCH_SET, "there is no binding set %u", set);
+    hipStream_t s = k->ctx->stream;
+    int slice = -1;
+    if (timer) {
+        int r = bl_timer_slice_begin(timer, tag, s, &slice);
+        if (r) return r;
+    }
+    hipError_t e = launch(k->kernels[kernel].per_set[set], s);
+    if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[kernel].label.c_str());
+    if (timer && slice >= 0) bl_timer_slice_end(timer, slice, s);
+    return BL_OK;
+}
+
+extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set) {
+    if (!k) return BL_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)first + count > k->kernels.size())
+        return fail(k->ctx, BL_ERR_NO_SUCH_KERNEL, "there is no kernel %u", first + count - 1);
+    if (set >= k->sets) return fail(k->ctx, BL_ERR_NO_SUCH_SET, "there is no binding set %u", set);
+    for (uint32_t i = first; i < first + count; i++) {
+        hipError_t e = launch(k->kernels[i].per_set[set], k->ctx->stream);
+        if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
+    }
+    return BL_OK;
+}
+
+extern "C" int bl_spin(bl_ctx *ctx, uint32_t micros) {
+    if (!ctx) return BL_ERR_INVALID_ARGUMENT;
+    if (!ctx->wall_clock_khz) return fail(ctx, BL_ERR_HIP, "the device reports no wall clock rate");
+    uint64_t ticks = (uint64_t)micros * ctx->wall_clock_khz / 1000;
+    hipError_t e = launch_spin(ticks, ctx->compute_units * 4, ctx->stream);
+    return e == hipSuccess ? BL_OK : hip_fail(ctx, e, "spin");
+}

@@ -1,0 +1,104 @@
+// Device-side helpers shared by the CDNA4 (gfx950) kernels: vector and MFMA
+// operand types, 64-lane wave reductions, the epilogue steps of a kernel spec
+// and GELU through erf.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "spec.hpp"
+
+namespace bl {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+
+// ---- loads/stores of one element as f32 ----
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
+
+// ---- 64-lane reductions (butterfly over the whole wave) ----
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+
+// ---- GELU through erf ----
+//
+// x * Phi(x) with Phi from erfc(|x| / sqrt 2) / 2, erfc by Abramowitz and
+// Stegun, Handbook of Mathematical Functions, formula 7.1.26 (|error| <=
+// 1.5e-7), the method and constants the reference's kernels use
+// (crates/beatlm-core/src/kernel.rs:335-372, codegen/wgsl.rs:331-353). The
+// negative side is a product, so nothing cancels.
+__device__ __forceinline__ float gelu_erf(float x) {
+    const float p = 0.3275911f;
+    const float a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f,
+                a4 = -1.453152027f, a5 = 1.061405429f;
+    float z = fabsf(x) * 0.70710678118654752f;
+    float t = 1.0f / (1.0f + p * z);
+    float poly = t * (a1 + t * (a2 + t * (a3 + t * (a4 + t * a5))));
+    float q = 0.5f * poly * __expf(-z * z);
+    return x * (x >= 0.0f ? 1.0f - q : q);
+}
+
+// GELU, tanh approximation (OpKind::Gelu, kernel.rs:934-942).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    u = fminf(fmaxf(u, -15.0f), 15.0f);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+
+// ---- epilogue: the spec's element-wise steps, in order, at an output index ----
+
+
+
+template <typename T>
+__device__ __forceinline__ float apply_epilogue(const EpilogueArgs &e, float v, uint64_t index) {
+    for (int s = 0; s < e.n; s++) {
+        switch (e.kind[s]) {
+        case BL_EPI_ADD: v = v + to_f32(((const T *)e.operand[s])[index]); break;
+        case BL_EPI_RELU: v = fmaxf(v, 0.0f); break;
+        case BL_EPI_GELU: v = gelu_tanh(v); break;
+        case BL_EPI_GELU_ERF: v = gelu_erf(v); break;
+        case BL_EPI_SCALE: v = v * e.factor[s]; break;
+        case BL_EPI_CHANNEL_SCALE:
+            v = v * to_f32(((const T *)e.operand[s])[index % e.channels[s]]);
+            break;
+        default: break;
+        }
+    }
+    return v;
+}
+
+// ---- splitting an f32 into two bf16s (hi + lo) ----
+//
+// hi = bf16(x), lo = bf16(x - hi): x - hi - lo is within 2^-16 |x|, so the
+// three products hi*hi + hi*lo + lo*hi of two split operands reproduce an f32
+// product to about 2^-15 relative (Henry, Tang and Heinecke, "Leveraging the
+// bfloat16 artificial intelligence datatype for higher-precision
+// computations", ARITH 2019).
+__device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
+    hi = (__bf16)x;
+    lo = (__bf16)(x - (float)hi);
+}
+
+}  // namespace bl

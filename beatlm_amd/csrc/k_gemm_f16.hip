@@ -1,0 +1,6 @@
+// The MFMA GEMM instantiated for Math::F16.
+#include "k_gemm.inc"
+
+namespace bl {
+hipError_t launch_gemm_f16(const GemmArgs &a, int tile, hipStream_t s) { return launch_math<Math::F16>(a, tile, s); }
+}  // namespace bl

@@ -1,0 +1,325 @@
+// The bandwidth-bound and vector-ALU kernels: layer norm, the standalone
+// softmax, the tiled products with gathered operands (unfused attention
+// scores and values, the patch embedding), one-element-per-invocation kernels
+// (standalone map, class-token prepend, token drop) and a fixed-time spin.
+#include "device_common.hpp"
+
+namespace bl {
+namespace {
+
+// ------------------------------------------------------------------------
+// Layer norm (MainOp::LayerNorm, kernel.rs:643-659; reference arithmetic
+// wgsl.rs:519-585): (x - mean) * rsqrt(var + eps) * gamma + beta per row,
+// mean first, then the biased variance of (x - mean).
+//
+// One wave per row, four rows per workgroup. A lane keeps its share of the
+// row in registers (16-byte loads, the row read from HBM once), so the two
+// passes and the store cost one read and one write of the row.
+// ------------------------------------------------------------------------
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void layernorm_kernel(LayerNormArgs a) {
+    constexpr int VEC = 16 / sizeof(T);
+    using V = typename std::conditional<sizeof(T) == 4, f32x4, f16x8>::type;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row = a.row0 + blockIdx.x * 4 + wave;
+    if (row >= a.row1) return;
+    const uint32_t C = a.channels, nch = C / VEC;
+    const T *x = (const T *)a.x + (uint64_t)row * C;
+    float v[NV][VEC];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        uint32_t c = lane + 64 * i;
+        V chunk = {};
+        if (c < nch) chunk = *(const V *)(x + c * VEC);
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            v[i][e] = to_f32(chunk[e]);
+            sum += v[i][e];
+        }
+    }
+    const float mean = wave_sum(sum) / (float)C;
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        if (lane + 64 * i < nch) {
+#pragma unroll
+            for (int e = 0; e < VEC; e++) {
+                float d = v[i][e] - mean;
+                sq += d * d;
+            }
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)C + a.eps);
+    const T *gamma = (const T *)a.gamma, *beta = (const T *)a.beta;
+    T *y = (T *)a.y + (uint64_t)row * C;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        uint32_t c = lane + 64 * i;
+        if (c >= nch) continue;
+        V gv = *(const V *)(gamma + c * VEC), bv = *(const V *)(beta + c * VEC);
+        V out;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            float r = (v[i][e] - mean) * inv * to_f32(gv[e]) + to_f32(bv[e]);
+            if (a.epi.n) r = apply_epilogue<T>(a.epi, r, (uint64_t)row * C + c * VEC + e);
+            out[e] = from_f32<T>(r);
+        }
+        *(V *)(y + c * VEC) = out;
+    }
+}
+
+// Any width: three passes over the row in memory, one wave per row.
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_any_kernel(LayerNormArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t row = a.row0 + blockIdx.x * 4 + wave;
+    if (row >= a.row1) return;
+    const uint32_t C = a.channels;
+    const T *x = (const T *)a.x + (uint64_t)row * C;
+    float sum = 0.0f;
+    for (uint32_t c = lane; c < C; c += 64) sum += to_f32(x[c]);
+    const float mean = wave_sum(sum) / (float)C;
+    float sq = 0.0f;
+    for (uint32_t c = lane; c < C; c += 64) {
+        float d = to_f32(x[c]) - mean;
+        sq += d * d;
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)C + a.eps);
+    const T *gamma = (const T *)a.gamma, *beta = (const T *)a.beta;
+    T *y = (T *)a.y + (uint64_t)row * C;
+    for (uint32_t c = lane; c < C; c += 64) {
+        float r = (to_f32(x[c]) - mean) * inv * to_f32(gamma[c]) + to_f32(beta[c]);
+        r = apply_epilogue<T>(a.epi, r, (uint64_t)row * C + c);
+        y[c] = from_f32<T>(r);
+    }
+}
+
+template <typename T>
+hipError_t ln_launch(const LayerNormArgs &a, hipStream_t s) {
+    constexpr uint32_t VEC = 16 / sizeof(T);
+    dim3 grid((a.row1 - a.row0 + 3) / 4), block(256);
+    const uint32_t nch = a.channels / VEC;
+    if (a.channels % VEC == 0) {
+        if (nch <= 64) { hipLaunchKernelGGL((layernorm_kernel<T, 1>), grid, block, 0, s, a); return hipGetLastError(); }
+        if (nch <= 128) { hipLaunchKernelGGL((layernorm_kernel<T, 2>), grid, block, 0, s, a); return hipGetLastError(); }
+        if (nch <= 256) { hipLaunchKernelGGL((layernorm_kernel<T, 4>), grid, block, 0, s, a); return hipGetLastError(); }
+    }
+    hipLaunchKernelGGL(layernorm_any_kernel<T>, grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------
+// Softmax over rows (MainOp::Softmax, kernel.rs:748-756; wgsl.rs:590-669):
+// exp(x - rowmax) / sum exp(x - rowmax). One workgroup per row; the unfused
+// attention path only (the block runs the flash kernel).
+// ------------------------------------------------------------------------
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float *scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = is_max ? wave_max(v) : wave_sum(v);
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float r = scratch[0];
+    for (int w = 1; w < (int)(blockDim.x / 64); w++) r = is_max ? fmaxf(r, scratch[w]) : r + scratch[w];
+    return r;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void softmax_kernel(SoftmaxArgs a) {
+    __shared__ float scratch[4];
+    const uint32_t row = a.row0 + blockIdx.x;
+    if (row >= a.row1) return;
+    const uint32_t C = a.cols;
+    const T *x = (const T *)a.x + (uint64_t)row * C;
+    float m = -INFINITY;
+    for (uint32_t c = threadIdx.x; c < C; c += 256) m = fmaxf(m, to_f32(x[c]));
+    m = block_reduce(m, true, scratch);
+    float sum = 0.0f;
+    for (uint32_t c = threadIdx.x; c < C; c += 256) sum += __expf(to_f32(x[c]) - m);
+    sum = block_reduce(sum, false, scratch);
+    const float inv = 1.0f / sum;
+    T *y = (T *)a.y + (uint64_t)row * C;
+    for (uint32_t c = threadIdx.x; c < C; c += 256) {
+        uint64_t i = (uint64_t)row * C + c;
+        y[c] = from_f32<T>(apply_epilogue<T>(a.epi, __expf(to_f32(x[c]) - m) * inv, i));
+    }
+}
+
+// ------------------------------------------------------------------------
+// Tiled products with gathered operands on the vector ALUs: the unfused
+// attention scores (one product per head, kernel.rs:731-741), the unfused
+// weighted sum of the values (kernel.rs:765-777) and the patch embedding as a
+// product of the gathered patches by the HWIO weights (kernel.rs:661-687).
+// 64 x 64 output tile, 16 reduction indices staged per step, 4 x 4 outputs
+// per invocation; each output summed over k in increasing order.
+// ------------------------------------------------------------------------
+template <Gather G, typename T>
+__device__ __forceinline__ float gather_a(const GatherArgs &a, uint32_t row, uint32_t kk, uint32_t layer) {
+    const T *A = (const T *)a.a;
+    if constexpr (G == Gather::SCORES) {
+        const uint32_t H = a.p1, D = a.p2;
+        return to_f32(A[(uint64_t)row * 3 * H * D + layer * D + kk]);
+    } else if constexpr (G == Gather::VALUES) {
+        const uint32_t Tn = a.p0, H = a.p1;
+        return to_f32(A[((uint64_t)row * H + layer) * Tn + kk]);
+    } else {
+        const uint32_t gw = a.p0, p = a.p1, cin = a.p2, width = a.p3;
+        uint32_t gy = row / gw, gx = row % gw;
+        uint32_t ky = kk / (p * cin), kx = (kk / cin) % p, ci = kk % cin;
+        return to_f32(A[((uint64_t)(gy * p + ky) * width + gx * p + kx) * cin + ci]);
+    }
+}
+template <Gather G, typename T>
+__device__ __forceinline__ float gather_b(const GatherArgs &a, uint32_t kk, uint32_t col, uint32_t layer) {
+    const T *B = (const T *)a.b;
+    if constexpr (G == Gather::SCORES) {
+        const uint32_t H = a.p1, D = a.p2;
+        return to_f32(B[(uint64_t)col * 3 * H * D + H * D + layer * D + kk]);
+    } else if constexpr (G == Gather::VALUES) {
+        const uint32_t H = a.p1, D = a.p2;
+        return to_f32(B[(uint64_t)kk * 3 * H * D + 2 * H * D + layer * D + col]);
+    } else {
+        return to_f32(B[(uint64_t)kk * a.n + col]);
+    }
+}
+template <Gather G>
+__device__ __forceinline__ uint64_t gather_out(const GatherArgs &a, uint32_t row, uint32_t col, uint32_t layer) {
+    if constexpr (G == Gather::SCORES) {
+        return ((uint64_t)row * a.p1 + layer) * a.p0 + col;
+    } else if constexpr (G == Gather::VALUES) {
+        return (uint64_t)row * a.p1 * a.p2 + layer * a.p2 + col;
+    } else {
+        return (uint64_t)row * a.n + col;
+    }
+}
+
+template <Gather G, typename T>
+__global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
+    constexpr int TR = 64, TC = 64, TD = 16;
+    __shared__ float As[TD][TR + 4];
+    __shared__ float Bs[TD][TC + 4];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const uint32_t row0 = a.row0 + blockIdx.y * TR, col0 = blockIdx.x * TC, layer = blockIdx.z;
+    float acc[4][4] = {};
+    for (uint32_t k0 = 0; k0 < a.k; k0 += TD) {
+        for (int e = threadIdx.x; e < TR * TD; e += 256) {
+            int kk = e % TD, r = e / TD;
+            uint32_t row = row0 + r, k = k0 + kk;
+            As[kk][r] = (row < a.row1 && k < a.k) ? gather_a<G, T>(a, row, k, layer) : 0.0f;
+        }
+        for (int e = threadIdx.x; e < TD * TC; e += 256) {
+            int kk, c;
+            if (G == Gather::SCORES) { kk = e % TD; c = e / TD; }  // keys: k contiguous
+            else { c = e % TC; kk = e / TC; }
+            uint32_t col = col0 + c, k = k0 + kk;
+            Bs[kk][c] = (col < a.n && k < a.k) ? gather_b<G, T>(a, k, col, layer) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < TD; kk++) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) av[i] = As[kk][ty * 4 + i];
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] += av[i] * bv[j];
+        }
+        __syncthreads();
+    }
+    const T *bias = (const T *)a.bias;
+    T *C = (T *)a.c;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t row = row0 + ty * 4 + i;
+        if (row >= a.row1) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t col = col0 + tx * 4 + j;
+            if (col >= a.n) continue;
+            float v = acc[i][j] + (bias ? to_f32(bias[col]) : 0.0f);
+            uint64_t idx = gather_out<G>(a, row, col, layer);
+            C[idx] = from_f32<T>(apply_epilogue<T>(a.epi, v, idx));
+        }
+    }
+}
+
+// ------------------------------------------------------------------------
+// One output element per invocation over the part's elements.
+// ------------------------------------------------------------------------
+template <PerElement P, typename T>
+__global__ __launch_bounds__(256) void element_kernel(ElementArgs a) {
+    const T *A = (const T *)a.a, *B = (const T *)a.b;
+    T *Y = (T *)a.y;
+    for (uint64_t i = a.start + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < a.end;
+         i += (uint64_t)gridDim.x * 256) {
+        float v;
+        if constexpr (P == PerElement::MAP) v = to_f32(A[i]);
+        else if constexpr (P == PerElement::PREPEND) v = i < a.channels ? to_f32(A[i]) : to_f32(B[i - a.channels]);
+        else v = to_f32(A[i + a.channels]);
+        Y[i] = from_f32<T>(apply_epilogue<T>(a.epi, v, i));
+    }
+}
+
+// Spins until `ticks` of the device's constant-rate wall clock have passed.
+__global__ void spin_kernel(uint64_t ticks) {
+    const uint64_t t0 = wall_clock64();
+    while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(1);
+}
+
+}  // namespace
+
+hipError_t launch_layernorm(const LayerNormArgs &a, bool f16, hipStream_t s) {
+    if (a.row1 <= a.row0) return hipSuccess;
+    return f16 ? ln_launch<_Float16>(a, s) : ln_launch<float>(a, s);
+}
+
+hipError_t launch_softmax(const SoftmaxArgs &a, bool f16, hipStream_t s) {
+    if (a.row1 <= a.row0) return hipSuccess;
+    dim3 grid(a.row1 - a.row0);
+    if (f16) hipLaunchKernelGGL(softmax_kernel<_Float16>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(softmax_kernel<float>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const GatherArgs &a, Gather g, bool f16, hipStream_t s) {
+    if (a.row1 <= a.row0) return hipSuccess;
+    dim3 grid((a.n + 63) / 64, (a.row1 - a.row0 + 63) / 64, a.layers);
+#define BL_GATHER(G)                                                                     \
+    if (f16) hipLaunchKernelGGL((gather_kernel<G, _Float16>), grid, dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((gather_kernel<G, float>), grid, dim3(256), 0, s, a);
+    switch (g) {
+    case Gather::SCORES: BL_GATHER(Gather::SCORES) break;
+    case Gather::VALUES: BL_GATHER(Gather::VALUES) break;
+    default: BL_GATHER(Gather::PATCH) break;
+    }
+#undef BL_GATHER
+    return hipGetLastError();
+}
+
+hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s) {
+    if (a.end <= a.start) return hipSuccess;
+    uint64_t blocks = (a.end - a.start + 255) / 256;
+    if (blocks > 65535) blocks = 65535;
+    dim3 grid((uint32_t)blocks);
+#define BL_ELEM(P)                                                                        \
+    if (f16) hipLaunchKernelGGL((element_kernel<P, _Float16>), grid, dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((element_kernel<P, float>), grid, dim3(256), 0, s, a);
+    switch (p) {
+    case PerElement::MAP: BL_ELEM(PerElement::MAP) break;
+    case PerElement::PREPEND: BL_ELEM(PerElement::PREPEND) break;
+    default: BL_ELEM(PerElement::DROP_FIRST) break;
+    }
+#undef BL_ELEM
+    return hipGetLastError();
+}
+
+hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s) {
+    hipLaunchKernelGGL(spin_kernel, dim3(blocks), dim3(64), 0, s, ticks);
+    return hipGetLastError();
+}
+
+}  // namespace bl

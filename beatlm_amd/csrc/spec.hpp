@@ -1,0 +1,116 @@
+// Internal: the launch arguments of each device kernel and the host-side
+// launchers the backend dispatches a kernel spec to.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/beatlm_hip.h"
+
+namespace bl {
+
+struct DevEpilogue;
+
+// How an f32 or f16 product is computed on the matrix cores.
+enum class Math : int {
+    F32 = 0,    // f32 storage, v_mfma_f32_16x16x4_f32
+    SPLIT = 1,  // f32 storage, each operand hi + lo bf16, three v_mfma_f32_16x16x32_bf16
+    F16 = 2,    // f16 storage, v_mfma_f32_16x16x32_f16, f32 accumulate
+};
+
+struct EpilogueArgs {
+    int n;
+    int kind[BL_MAX_EPILOGUE];
+    float factor[BL_MAX_EPILOGUE];
+    uint32_t channels[BL_MAX_EPILOGUE];
+    const void *operand[BL_MAX_EPILOGUE];
+};
+
+struct LayerNormArgs {
+    const void *x, *gamma, *beta;
+    void *y;
+    uint32_t rows, channels;
+    uint32_t row0, row1;  // the part's rows
+    float eps;
+    EpilogueArgs epi;
+};
+
+struct GemmArgs {
+    const void *a, *b, *bias;
+    void *c;
+    uint32_t m, n, k;
+    uint32_t row0, row1;
+    EpilogueArgs epi;
+};
+
+// The tiled products whose operands are gathered (the unfused attention
+// products and the patch embedding), on the vector ALUs.
+enum class Gather : int { SCORES = 0, VALUES = 1, PATCH = 2 };
+
+struct GatherArgs {
+    const void *a, *b, *bias;
+    void *c;
+    uint32_t n, k, layers;          // output columns per layer, reduction, layers
+    uint32_t row0, row1;
+    // attention: tokens, heads, head_dim; patch: grid_w, patch, cin, image width
+    uint32_t p0, p1, p2, p3;
+    EpilogueArgs epi;
+};
+
+struct SoftmaxArgs {
+    const void *x;
+    void *y;
+    uint32_t cols;
+    uint32_t row0, row1;
+    EpilogueArgs epi;
+};
+
+struct FlashArgs {
+    const void *qkv;
+    void *out;
+    float *partial;       // [splits][tokens][heads][64] f32, when splits > 1
+    float *stats;         // [splits][tokens][heads][2] (max, sum), when splits > 1
+    uint32_t tokens, heads;
+    uint32_t row0, row1;  // query rows of the part
+    uint32_t splits;
+    float scale;          // softmax scale (the Scale epilogue of the scores)
+};
+
+// One element per invocation: the standalone map, the token copies.
+enum class PerElement : int { MAP = 0, PREPEND = 1, DROP_FIRST = 2 };
+
+struct ElementArgs {
+    const void *a, *b;
+    void *y;
+    uint64_t start, end;  // output elements of the part
+    uint32_t channels;
+    EpilogueArgs epi;
+};
+
+// ---- launchers (one per kernel family), defined with their kernels ----
+
+hipError_t launch_layernorm(const LayerNormArgs &a, bool f16, hipStream_t s);
+hipError_t launch_gemm_f32(const GemmArgs &a, int tile, hipStream_t s);
+hipError_t launch_gemm_split(const GemmArgs &a, int tile, hipStream_t s);
+hipError_t launch_gemm_f16(const GemmArgs &a, int tile, hipStream_t s);
+inline hipError_t launch_gemm(const GemmArgs &a, Math m, int tile, hipStream_t s) {
+    if (a.row1 <= a.row0) return hipSuccess;
+    return m == Math::F32 ? launch_gemm_f32(a, tile, s)
+         : m == Math::SPLIT ? launch_gemm_split(a, tile, s) : launch_gemm_f16(a, tile, s);
+}
+hipError_t launch_gather(const GatherArgs &a, Gather g, bool f16, hipStream_t s);
+hipError_t launch_softmax(const SoftmaxArgs &a, bool f16, hipStream_t s);
+hipError_t launch_flash(const FlashArgs &a, Math m, hipStream_t s);
+hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s);
+hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
+
+// GEMM tile shapes the dispatcher can pick from: BM x BN.
+enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x128 = 3, TILE_128x64 = 4, TILE_COUNT = 5 };
+inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128}; return r[t]; }
+inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 128, 64}; return c[t]; }
+
+// The flash kernel's query rows per workgroup.
+constexpr uint32_t FLASH_ROWS = 64;
+constexpr uint32_t FLASH_HEAD_DIM = 64;
+
+}  // namespace bl

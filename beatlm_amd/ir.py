@@ -1,0 +1,441 @@
+"""ctypes binding of the IR's C API (include/beatlm_ir.h) and the harness that
+runs a graph through the backend, as the reference's
+`harness::run_on_gpu` does (crates/beatlm-bench/src/harness.rs:133-172):
+lower -> (fuse attention) -> split -> plan -> arenas -> write -> kernels ->
+encode -> read.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import hip
+from .hip import Spec, lib
+
+NONE = 0xFFFFFFFF
+
+INPUT, WEIGHT, ACTIVATION, OUTPUT = 0, 1, 2, 3
+FUSION_ON, FUSION_OFF = 0, 1
+
+OP_LAYER_NORM = 1
+OP_MATMUL = 2
+OP_ATTENTION_SCORES = 3
+OP_SOFTMAX = 4
+OP_ATTENTION_VALUES = 5
+OP_PATCH_EMBED = 6
+OP_PREPEND_TOKEN = 7
+OP_TOKENS_TO_MAP = 8
+OP_ADD = 20
+OP_RELU = 21
+OP_GELU = 22
+OP_GELU_ERF = 23
+OP_SCALE = 24
+OP_CHANNEL_SCALE = 25
+
+ERRORS = {
+    -100: "DuplicateTensor", -101: "EmptyTensor", -102: "TensorTooLarge", -103: "UnknownTensor",
+    -104: "ElementCount", -105: "ReadBeforeWritten", -106: "WrittenTwice", -107: "NotWritable",
+    -108: "ZeroDimension", -109: "OpTooLarge", -110: "NonFiniteScale", -111: "InvalidEpsilon",
+    -112: "TooManyOps", -113: "EmptyGraph", -114: "NeverWritten", -115: "NotInputOrOutput",
+    -116: "ExceedsLimit", -117: "PartCounts", -118: "AlreadySplit", -119: "ZeroBound", -120: "UnknownOp",
+    -130: "Plan.DuplicateTensor", -131: "Plan.InvalidLifetime", -132: "Plan.EmptyTensor",
+    -133: "Plan.SizeOverflow", -134: "Plan.TensorTooLarge", -135: "Plan.InvalidProfile",
+    -136: "Plan.TooManyTensors", -137: "NoPlacement",
+}
+
+
+class Op(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("t", C.c_uint32 * 4), ("d", C.c_uint32 * 6), ("f", C.c_float)]
+
+
+def op(kind: int, tensors, dims, f: float = 0.0) -> Op:
+    o = Op()
+    o.kind = kind
+    t = list(tensors) + [NONE] * (4 - len(tensors))
+    d = list(dims) + [0] * (6 - len(dims))
+    o.t = (C.c_uint32 * 4)(*t)
+    o.d = (C.c_uint32 * 6)(*d)
+    o.f = f
+    return o
+
+
+class TensorDesc(C.Structure):
+    _fields_ = [
+        ("id", C.c_uint32),
+        ("dtype", C.c_uint32),
+        ("elements", C.c_uint64),
+        ("first_use", C.c_uint32),
+        ("last_use", C.c_uint32),
+    ]
+
+
+class Profile(C.Structure):
+    _fields_ = [
+        ("max_storage_buffer_binding_size", C.c_uint64),
+        ("max_buffer_size", C.c_uint64),
+        ("min_storage_buffer_offset_alignment", C.c_uint32),
+        ("max_compute_workgroup_storage_size", C.c_uint32),
+        ("max_compute_invocations_per_workgroup", C.c_uint32),
+        ("max_compute_workgroups_per_dimension", C.c_uint32),
+        ("max_storage_buffers_per_shader_stage", C.c_uint32),
+    ]
+
+
+class Placement(C.Structure):
+    _fields_ = [("arena", C.c_uint32), ("reserved", C.c_uint32), ("offset", C.c_uint64), ("size", C.c_uint64)]
+
+
+class KernelInfo(C.Structure):
+    _fields_ = [
+        ("main", C.c_uint32),
+        ("dims", C.c_uint32 * 6),
+        ("epsilon", C.c_float),
+        ("scale", C.c_float),
+        ("part", hip.Part),
+        ("max_parts", C.c_uint32),
+        ("tile_rows", C.c_uint32),
+        ("output_start", C.c_uint64),
+        ("output_end", C.c_uint64),
+        ("n_reads", C.c_uint32),
+        ("reads", C.c_uint32 * 4),
+        ("n_epilogue", C.c_uint32),
+        ("epilogue", hip.Epilogue * hip.MAX_EPILOGUE),
+        ("n_bindings", C.c_uint32),
+        ("bindings", C.c_uint32 * hip.MAX_BINDINGS),
+        ("first_op", C.c_uint32),
+        ("end_op", C.c_uint32),
+    ]
+
+
+class VitDims(C.Structure):
+    _fields_ = [
+        ("tokens", C.c_uint32),
+        ("width", C.c_uint32),
+        ("heads", C.c_uint32),
+        ("mlp", C.c_uint32),
+        ("epsilon", C.c_float),
+    ]
+
+
+BLOCK_WEIGHTS = (
+    "norm1_g", "norm1_b", "qkv_w", "qkv_b", "proj_w", "proj_b", "ls1",
+    "norm2_g", "norm2_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b", "ls2",
+)
+
+
+class BlockIds(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in BLOCK_WEIGHTS] + [("output", C.c_uint32), ("next_id", C.c_uint32)]
+
+
+class EmbedIds(C.Structure):
+    _fields_ = [
+        (n, C.c_uint32) for n in ("image", "patch_w", "patch_b", "cls", "pos", "output", "next_id")
+    ]
+
+
+_VP = C.c_void_p
+_SIG = {
+    "bli_last_error": (C.c_char_p, []),
+    "bli_profile_webgpu_baseline": (None, [C.POINTER(Profile)]),
+    "bli_profile_mi355x": (None, [C.POINTER(Profile)]),
+    "bli_graph_new": (C.c_int, [C.POINTER(_VP)]),
+    "bli_graph_free": (None, [_VP]),
+    "bli_graph_tensor": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint64]),
+    "bli_graph_push": (C.c_int, [_VP, C.POINTER(Op), C.c_uint32]),
+    "bli_op_output_elements": (C.c_uint64, [C.POINTER(Op)]),
+    "bli_graph_ops": (C.c_uint32, [_VP]),
+    "bli_graph_lower": (C.c_int, [_VP, C.c_uint32, C.POINTER(_VP)]),
+    "bli_program_free": (None, [_VP]),
+    "bli_program_split": (C.c_int, [_VP, C.POINTER(C.c_uint32), C.c_uint32, C.POINTER(_VP)]),
+    "bli_program_parts_within": (
+        C.c_int, [_VP, C.POINTER(C.c_uint64), C.c_uint32, C.c_uint64, C.POINTER(C.c_uint32)]
+    ),
+    "bli_program_fuse_attention": (C.c_int, [_VP, C.POINTER(_VP)]),
+    "bli_program_set_dtype": (C.c_int, [_VP, C.c_uint32]),
+    "bli_program_len": (C.c_uint32, [_VP]),
+    "bli_program_kernel": (C.c_int, [_VP, C.c_uint32, C.POINTER(KernelInfo)]),
+    "bli_program_kernel_name": (C.c_int, [_VP, C.c_uint32, C.c_char_p, C.c_uint32]),
+    "bli_program_tensors": (C.c_uint32, [_VP, C.POINTER(TensorDesc), C.c_uint32]),
+    "bli_program_role": (C.c_int, [_VP, C.c_uint32]),
+    "bli_program_stand_in": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.POINTER(TensorDesc)]),
+    "bli_program_spec": (C.c_int, [_VP, C.c_uint32, _VP, C.POINTER(Spec)]),
+    "bli_plan_new": (C.c_int, [C.POINTER(TensorDesc), C.c_uint32, C.POINTER(Profile), C.POINTER(_VP)]),
+    "bli_plan_free": (None, [_VP]),
+    "bli_plan_arenas": (C.c_uint32, [_VP, C.POINTER(C.c_uint64), C.c_uint32]),
+    "bli_plan_placement": (C.c_int, [_VP, C.c_uint32, C.POINTER(Placement)]),
+    "bli_plan_peak_live_bytes": (C.c_uint64, [_VP]),
+    "bli_plan_total_bytes": (C.c_uint64, [_VP]),
+    "bli_plan_valid_on": (C.c_int, [_VP, C.POINTER(Profile)]),
+    "bli_vit_block": (C.c_int, [_VP, C.POINTER(VitDims), C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(BlockIds)]),
+    "bli_vit_embeddings": (
+        C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(EmbedIds)]
+    ),
+}
+_bound = False
+
+
+def _lib():
+    global _bound
+    h = lib()
+    if not _bound:
+        for name, (res, args) in _SIG.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _bound = True
+    return h
+
+
+class IrError(RuntimeError):
+    def __init__(self, code: int):
+        self.code = code
+        self.kind = ERRORS.get(code, str(code))
+        super().__init__(f"{self.kind}: {_lib().bli_last_error().decode()}")
+
+
+def _check(rc: int) -> int:
+    if rc < 0:
+        raise IrError(rc)
+    return rc
+
+
+def profile(kind: str = "mi355x") -> Profile:
+    p = Profile()
+    if kind == "baseline":
+        _lib().bli_profile_webgpu_baseline(C.byref(p))
+    else:
+        _lib().bli_profile_mi355x(C.byref(p))
+    return p
+
+
+class Graph:
+    def __init__(self):
+        h = C.c_void_p()
+        _check(_lib().bli_graph_new(C.byref(h)))
+        self.handle = h
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            _lib().bli_graph_free(self.handle)
+            self.handle = None
+
+    def tensor(self, tid: int, role: int, elements: int) -> int:
+        _check(_lib().bli_graph_tensor(self.handle, tid, role, elements))
+        return tid
+
+    def push(self, o: Op, output: int) -> int:
+        _check(_lib().bli_graph_push(self.handle, C.byref(o), output))
+        return output
+
+    def ops(self) -> int:
+        return int(_lib().bli_graph_ops(self.handle))
+
+    def lower(self, fusion: int = FUSION_ON) -> "Program":
+        h = C.c_void_p()
+        _check(_lib().bli_graph_lower(self.handle, fusion, C.byref(h)))
+        return Program(h)
+
+    def vit_block(self, dims: VitDims, x: int, first_id: int, role: int = ACTIVATION) -> BlockIds:
+        ids = BlockIds()
+        _check(_lib().bli_vit_block(self.handle, C.byref(dims), x, first_id, role, C.byref(ids)))
+        return ids
+
+    def vit_embeddings(self, grid: int, patch: int, channels: int, width: int, first_id: int) -> EmbedIds:
+        ids = EmbedIds()
+        _check(_lib().bli_vit_embeddings(self.handle, grid, patch, channels, width, first_id, C.byref(ids)))
+        return ids
+
+
+def output_elements(o: Op) -> int:
+    return int(_lib().bli_op_output_elements(C.byref(o)))
+
+
+class Program:
+    def __init__(self, handle):
+        self.handle = handle
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            _lib().bli_program_free(self.handle)
+            self.handle = None
+
+    def __len__(self) -> int:
+        return int(_lib().bli_program_len(self.handle))
+
+    def split(self, parts) -> "Program":
+        arr = (C.c_uint32 * max(1, len(parts)))(*parts)
+        h = C.c_void_p()
+        _check(_lib().bli_program_split(self.handle, arr, len(parts), C.byref(h)))
+        return Program(h)
+
+    def parts_within(self, durations_us, bound_us: int) -> list[int]:
+        arr = (C.c_uint64 * max(1, len(durations_us)))(*durations_us)
+        out = (C.c_uint32 * max(1, len(durations_us)))()
+        _check(_lib().bli_program_parts_within(self.handle, arr, len(durations_us), bound_us, out))
+        return list(out[: len(durations_us)])
+
+    def fuse_attention(self) -> "Program":
+        h = C.c_void_p()
+        _check(_lib().bli_program_fuse_attention(self.handle, C.byref(h)))
+        return Program(h)
+
+    def set_dtype(self, dtype: int) -> "Program":
+        _check(_lib().bli_program_set_dtype(self.handle, dtype))
+        return self
+
+    def kernel(self, k: int) -> KernelInfo:
+        info = KernelInfo()
+        _check(_lib().bli_program_kernel(self.handle, k, C.byref(info)))
+        return info
+
+    def name(self, k: int) -> str:
+        buf = C.create_string_buffer(256)
+        _check(_lib().bli_program_kernel_name(self.handle, k, buf, 256))
+        return buf.value.decode()
+
+    def names(self) -> list[str]:
+        return [self.name(k) for k in range(len(self))]
+
+    def bindings(self, k: int) -> list[int]:
+        info = self.kernel(k)
+        return list(info.bindings[: info.n_bindings])
+
+    def tensors(self) -> list[TensorDesc]:
+        n = _lib().bli_program_tensors(self.handle, None, 0)
+        arr = (TensorDesc * max(1, n))()
+        _lib().bli_program_tensors(self.handle, arr, n)
+        return list(arr[:n])
+
+    def lifetime(self, tid: int):
+        for t in self.tensors():
+            if t.id == tid:
+                return (t.first_use, t.last_use)
+        return None
+
+    def role(self, tid: int) -> int:
+        return int(_lib().bli_program_role(self.handle, tid))
+
+    def stand_in(self, of: int, tid: int) -> TensorDesc:
+        d = TensorDesc()
+        _check(_lib().bli_program_stand_in(self.handle, of, tid, C.byref(d)))
+        return d
+
+    def spec(self, k: int, plan: "Plan") -> Spec:
+        s = Spec()
+        _check(_lib().bli_program_spec(self.handle, k, plan.handle, C.byref(s)))
+        return s
+
+    def specs(self, plan: "Plan") -> list[Spec]:
+        return [self.spec(k, plan) for k in range(len(self))]
+
+
+class Plan:
+    def __init__(self, tensors, prof: Profile | None = None):
+        prof = prof or profile("mi355x")
+        arr = (TensorDesc * max(1, len(tensors)))(*tensors)
+        h = C.c_void_p()
+        _check(_lib().bli_plan_new(arr, len(tensors), C.byref(prof), C.byref(h)))
+        self.handle = h
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            _lib().bli_plan_free(self.handle)
+            self.handle = None
+
+    def arenas(self) -> list[int]:
+        n = _lib().bli_plan_arenas(self.handle, None, 0)
+        arr = (C.c_uint64 * max(1, n))()
+        _lib().bli_plan_arenas(self.handle, arr, n)
+        return list(arr[:n])
+
+    def placement(self, tid: int) -> Placement | None:
+        p = Placement()
+        if _lib().bli_plan_placement(self.handle, tid, C.byref(p)) < 0:
+            return None
+        return p
+
+    def peak_live_bytes(self) -> int:
+        return int(_lib().bli_plan_peak_live_bytes(self.handle))
+
+    def total_bytes(self) -> int:
+        return int(_lib().bli_plan_total_bytes(self.handle))
+
+    def valid_on(self, prof: Profile) -> bool:
+        return bool(_lib().bli_plan_valid_on(self.handle, C.byref(prof)))
+
+
+def tensor_desc(tid, dtype, elements, first, last) -> TensorDesc:
+    return TensorDesc(tid, dtype, elements, first, last)
+
+
+# ---------------------------------------------------------------------------
+# running a graph on the device
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Prepared:
+    """A program realised on the device once: plan, arenas, kernels."""
+
+    ctx: hip.Context
+    program: Program
+    plan: Plan
+    arenas: hip.Arenas
+    kernels: hip.Kernels
+    dtype: int
+
+    def np_dtype(self):
+        return np.float16 if self.dtype == hip.F16 else np.float32
+
+    def write(self, tid: int, values: np.ndarray) -> None:
+        p = self.plan.placement(tid)
+        if p is None:
+            raise KeyError(f"tensor {tid} has no placement")
+        self.arenas.write(p.arena, p.offset, np.ascontiguousarray(values, dtype=self.np_dtype()))
+
+    def read(self, tid: int) -> np.ndarray:
+        p = self.plan.placement(tid)
+        elements = next(t.elements for t in self.program.tensors() if t.id == tid)
+        return self.arenas.read(p.arena, p.offset, elements, self.np_dtype())
+
+    def run(self, set_index: int = 0) -> None:
+        self.kernels.encode_all(set_index)
+
+
+def prepare(
+    ctx: hip.Context,
+    graph: Graph,
+    fusion: int = FUSION_ON,
+    parts: int = 1,
+    flash: bool = True,
+    dtype: int = hip.F32,
+) -> Prepared:
+    """Lower, optionally fuse attention, split every kernel into `parts`, plan
+    against the MI355X profile and build the kernels."""
+    program = graph.lower(fusion)
+    if flash:
+        program = program.fuse_attention()
+    if parts != 1:
+        program = program.split([parts] * len(program))
+    program.set_dtype(dtype)
+    plan = Plan(program.tensors(), profile("mi355x"))
+    arenas = hip.Arenas(ctx, plan.arenas())
+    kernels = hip.Kernels(ctx, arenas, program.specs(plan))
+    return Prepared(ctx, program, plan, arenas, kernels, dtype)
+
+
+def run_on_gpu(ctx, graph, values: dict[int, np.ndarray], fusion=FUSION_ON, parts=1, flash=True, dtype=hip.F32):
+    """The reference's harness::run_on_gpu: every output tensor's numbers."""
+    prep = prepare(ctx, graph, fusion, parts, flash, dtype)
+    for tid, v in values.items():
+        prep.write(tid, v)
+    prep.run()
+    ctx.synchronize()
+    outs = {}
+    for t in prep.program.tensors():
+        if prep.program.role(t.id) == OUTPUT:
+            outs[t.id] = prep.read(t.id).astype(np.float32)
+    return outs

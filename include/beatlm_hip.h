@@ -1,0 +1,282 @@
+/*
+ * beatlm HIP backend: the C ABI that replaces the reference's wgpu backend for
+ * one lowered program (a list of kernel specs over a memory plan) on one AMD
+ * Instinct MI355X (gfx950).
+ *
+ * The reference's boundary is everything below `&[KernelSpec] + &MemoryPlan`:
+ *
+ *   reference (Rust, crates/beatlm)                       this ABI
+ *   ---------------------------------------------------   ----------------------------
+ *   gpu::profile(limits, features)      gpu/profile.rs:24  bl_device_profile
+ *   Arenas::new(device, plan)           gpu/arenas.rs:88   bl_arenas_create
+ *   queue.write_buffer(arena, off, ..)  bench harness.rs:145-149  bl_arenas_write
+ *   (map_async readback, tests only)    bench harness.rs:95-121   bl_arenas_read
+ *   Kernels::new(device, plan, arenas,  codegen/kernels.rs:63-184 bl_kernels_create
+ *                specs, sets)
+ *   Kernels::encode(enc, k, set, ts)    codegen/kernels.rs:217-233 bl_kernels_encode
+ *   Kernels::{len, sets, label}         codegen/kernels.rs:188-209 bl_kernels_len/_sets/_label
+ *   SliceTimer::new(device, queue, n)   gpu/timer.rs:208    bl_timer_create
+ *   SliceTimer::begin_frame(frame)      gpu/timer.rs:272    bl_timer_begin_frame
+ *   FrameTimestamps::compute_pass(tag)  gpu/timer.rs:507    (timer argument of bl_kernels_encode)
+ *   FrameTimestamps::resolve(encoder)   gpu/timer.rs:561    bl_timer_resolve
+ *   SliceTimer::submitted(resolved)     gpu/timer.rs:307    bl_timer_submitted
+ *   SliceTimer::collect_ready()         gpu/timer.rs:371    bl_timer_collect
+ *   SliceTimer::invalidate_submitted()  gpu/timer.rs:445    bl_timer_invalidate_submitted
+ *   SliceTimer::stats()                 gpu/timer.rs:458    bl_timer_stats
+ *
+ * A `bl_spec` is the reference's `KernelSpec` (crates/beatlm-core/src/kernel.rs
+ * :1939-1947) flattened: main operation and its dimensions, the `Part` of the
+ * split dimension one dispatch computes, the epilogue steps in order, and the
+ * bindings in `KernelSpec::bindings` order (main reads, epilogue operands,
+ * output last; kernel.rs:2096-2113), each resolved through the memory plan to
+ * (arena, offset, size) as `Arenas::binding` does (gpu/arenas.rs:127-155).
+ *
+ * Conventions: every call returns a status, 0 = ok, negative = the error enum
+ * below (mirroring CodegenError, ArenaError, TimerError and KernelError);
+ * bl_last_error(ctx) gives the message of the last failure on that context.
+ * Handles are opaque and destroyed by the caller. A context is used from one
+ * thread at a time. Everything that allocates happens in the create calls;
+ * bl_kernels_encode allocates nothing and never waits for the GPU.
+ */
+#ifndef BEATLM_HIP_H
+#define BEATLM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BL_ABI_VERSION 1u
+#define BL_MAX_EPILOGUE 8
+#define BL_MAX_BINDINGS 8
+
+/* ---- status codes ---- */
+enum {
+    BL_OK = 0,
+    BL_ERR_HIP = -1,                   /* a HIP runtime call failed (device lost, OOM, ...) */
+    BL_ERR_INVALID_ARGUMENT = -2,      /* null pointer, zero count, bad enum */
+    /* ArenaError (gpu/arenas.rs:18-48) */
+    BL_ERR_PLAN_NOT_VALID_ON_DEVICE = -10,
+    BL_ERR_UNKNOWN_ARENA = -11,
+    BL_ERR_PLACEMENT_OUT_OF_RANGE = -12,
+    BL_ERR_MISALIGNED_PLACEMENT = -13,
+    /* CodegenError (codegen/mod.rs:85-154) */
+    BL_ERR_KERNEL = -20,               /* the spec has no variant that runs here */
+    BL_ERR_MISSING_PLACEMENT = -21,
+    BL_ERR_STAND_IN_SIZE = -22,
+    BL_ERR_NO_SUCH_KERNEL = -23,
+    BL_ERR_NO_SUCH_SET = -24,
+    /* TimerError (gpu/timer.rs:61-89) */
+    BL_ERR_TIMER_TOO_MANY_SLICES = -30,
+    BL_ERR_TIMER_NO_FRAME = -31,
+    BL_ERR_TIMER_CAPACITY = -32
+};
+
+/* ---- main operations (MainOp, kernel.rs:1393-1445) ---- */
+enum {
+    BL_MAIN_LAYER_NORM = 1,       /* dims: rows, channels; epsilon */
+    BL_MAIN_MATMUL = 2,           /* dims: m, k, n, has_bias */
+    BL_MAIN_ATTENTION_SCORES = 3, /* dims: tokens, heads, head_dim */
+    BL_MAIN_SOFTMAX = 4,          /* dims: rows, cols */
+    BL_MAIN_ATTENTION_VALUES = 5, /* dims: tokens, heads, head_dim */
+    BL_MAIN_PATCH_EMBED = 6,      /* dims: grid_h, grid_w, patch, cin, cout, has_bias */
+    BL_MAIN_PREPEND_TOKEN = 7,    /* dims: rows, channels */
+    BL_MAIN_TOKENS_TO_MAP = 8,    /* dims: height, width, channels */
+    BL_MAIN_MAP = 9,              /* dims: elements */
+    /* Backend-level main op with no MainOp counterpart: the three kernels
+     * attention_scores+scale -> softmax -> attention_values over one qkv tensor
+     * fused into one flash-attention kernel (online softmax, no [T][H][T]
+     * tensors). dims: tokens, heads, head_dim; scale = the Scale epilogue's
+     * factor. Bindings: qkv, output. Parts split along query rows. */
+    BL_MAIN_FLASH_ATTENTION = 100
+};
+
+/* ---- epilogue steps (Epilogue, kernel.rs:1593-1615) ---- */
+enum {
+    BL_EPI_ADD = 1,           /* v + operand[index] */
+    BL_EPI_RELU = 2,
+    BL_EPI_GELU = 3,          /* tanh approximation */
+    BL_EPI_GELU_ERF = 4,
+    BL_EPI_SCALE = 5,         /* v * factor */
+    BL_EPI_CHANNEL_SCALE = 6  /* v * operand[index % channels] */
+};
+
+/* ---- element types (DType, memory.rs:133-150) ---- */
+enum { BL_F32 = 0, BL_F16 = 1 };
+
+/* ---- how f32 products run on the matrix cores ---- */
+enum {
+    BL_F32_MATH_SPLIT_BF16 = 0, /* each f32 operand as hi + lo bf16, three bf16 MFMAs, f32 accumulate */
+    BL_F32_MATH_MFMA_F32 = 1    /* v_mfma_f32_*_f32: f32 operands, f32 accumulate */
+};
+
+typedef struct {
+    uint32_t kind;       /* BL_EPI_* */
+    float factor;        /* BL_EPI_SCALE */
+    uint32_t channels;   /* BL_EPI_CHANNEL_SCALE */
+    uint32_t operand;    /* binding index of the tensor read (ADD, CHANNEL_SCALE) */
+} bl_epilogue;
+
+typedef struct {
+    uint32_t tensor;     /* TensorId; what a binding set substitutes by */
+    uint32_t arena;      /* Placement::arena */
+    uint64_t offset;     /* Placement::offset (bytes) */
+    uint64_t size;       /* Placement::size (bytes) */
+    uint32_t dtype;      /* BL_F32 / BL_F16 */
+    uint32_t reserved;
+} bl_binding;
+
+typedef struct {
+    uint32_t index, count; /* Part::index, Part::count */
+    uint32_t start, end;   /* Part::range, in units of the split dimension */
+} bl_part;
+
+typedef struct {
+    uint32_t main;                 /* BL_MAIN_* */
+    uint32_t dims[6];              /* per main op, see the enum */
+    float epsilon;                 /* layer norm */
+    float scale;                   /* flash attention */
+    bl_part part;
+    /* Binding index of each tensor the main operation reads, in MainOp::reads
+     * order (kernel.rs:1447-1474); duplicates in `bindings` are allowed to
+     * collapse, as KernelSpec::bindings does. */
+    uint32_t n_reads;
+    uint32_t reads[4];
+    uint32_t n_epilogue;
+    bl_epilogue epilogue[BL_MAX_EPILOGUE];
+    uint32_t n_bindings;
+    bl_binding bindings[BL_MAX_BINDINGS];
+} bl_spec;
+
+/* One binding set: tensors of the specs bound to stand-ins (Substitution,
+ * codegen/kernels.rs:22-26), each given with the stand-in's placement. */
+typedef struct {
+    uint32_t original;   /* TensorId of the spec's binding */
+    uint32_t stand_in;   /* TensorId bound in its place */
+    uint32_t arena;
+    uint32_t reserved;
+    uint64_t offset, size;
+} bl_substitution;
+
+typedef struct {
+    const bl_substitution *items;
+    uint32_t count;
+} bl_binding_set;
+
+/* DeviceProfile (crates/beatlm-core/src/device.rs:62-95) as the device reports it. */
+typedef struct {
+    uint64_t max_storage_buffer_binding_size;
+    uint64_t max_buffer_size;
+    uint32_t min_storage_buffer_offset_alignment;
+    uint32_t max_compute_workgroup_storage_size;
+    uint32_t max_compute_invocations_per_workgroup;
+    uint32_t max_compute_workgroup_size[3];
+    uint32_t max_compute_workgroups_per_dimension;
+    uint32_t max_storage_buffers_per_shader_stage;
+    uint32_t shader_f16, subgroups, timestamp_query;
+    /* what the core profile has no field for */
+    uint32_t compute_units;
+    uint32_t wave_size;
+    uint64_t total_memory;
+    char name[64];
+    char arch[32];
+} bl_device_profile_t;
+
+typedef struct bl_ctx bl_ctx;
+typedef struct bl_arenas bl_arenas;
+typedef struct bl_kernels bl_kernels;
+typedef struct bl_timer bl_timer;
+
+/* ---- context ---- */
+uint32_t bl_abi_version(void);
+int bl_ctx_create(int device_ordinal, bl_ctx **out);
+void bl_ctx_destroy(bl_ctx *ctx);
+const char *bl_last_error(const bl_ctx *ctx);
+int bl_device_profile(bl_ctx *ctx, bl_device_profile_t *out);
+/* BL_F32_MATH_*; applies to kernels created afterwards. */
+int bl_ctx_set_f32_math(bl_ctx *ctx, uint32_t mode);
+/* Waits for everything submitted on the context's stream (tests and hosts
+ * outside the frame loop only). */
+int bl_ctx_synchronize(bl_ctx *ctx);
+/* Device allocations the context has made (arenas, scratch, events): the
+ * frame loop's count must not move. */
+uint64_t bl_ctx_allocations(const bl_ctx *ctx);
+/* The context's HIP stream (hipStream_t), for hosts that order their own work
+ * (e.g. a render pass) on it. */
+void *bl_ctx_stream(bl_ctx *ctx);
+
+/* ---- arenas: one hipMalloc for every arena of a plan ---- */
+int bl_arenas_create(bl_ctx *ctx, const uint64_t *arena_sizes, uint32_t n,
+                     bl_arenas **out);
+void bl_arenas_destroy(bl_arenas *arenas);
+/* Ordered on the context's stream; returns when the source may be reused. */
+int bl_arenas_write(bl_arenas *arenas, uint32_t arena, uint64_t offset,
+                    const void *src, uint64_t bytes);
+/* Waits for the stream, then copies out. */
+int bl_arenas_read(bl_arenas *arenas, uint32_t arena, uint64_t offset, void *dst,
+                   uint64_t bytes);
+/* Device address of a byte of an arena (for hosts that bind their own work). */
+int bl_arenas_device_ptr(bl_arenas *arenas, uint32_t arena, uint64_t offset,
+                         void **out);
+
+/* ---- kernels ---- */
+int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs,
+                      uint32_t n_specs, const bl_binding_set *sets,
+                      uint32_t n_sets, bl_kernels **out);
+void bl_kernels_destroy(bl_kernels *kernels);
+uint32_t bl_kernels_len(const bl_kernels *kernels);
+uint32_t bl_kernels_sets(const bl_kernels *kernels);
+/* The spec's name (e.g. "matmul+channel_scale+add"), followed for a part of a
+ * split kernel by " part i/n"; the variant chosen after " @ ". */
+const char *bl_kernels_label(const bl_kernels *kernels, uint32_t kernel);
+/* Launches kernel `kernel` with binding set `set` on the context's stream.
+ * With a timer, the launch is bracketed by that timer's events for the
+ * current frame under `tag`. No allocation, no wait. */
+int bl_kernels_encode(bl_kernels *kernels, uint32_t kernel, uint32_t set,
+                      bl_timer *timer, uint32_t tag);
+/* Launches kernels [first, first + count) in order with binding set `set`. */
+int bl_kernels_encode_range(bl_kernels *kernels, uint32_t first, uint32_t count,
+                            uint32_t set);
+
+/* ---- slice timer: hipEvent pairs per slice, a ring of frames ---- */
+#define BL_TIMER_RING_DEPTH 3
+typedef struct {
+    uint64_t frame;       /* FrameIndex given to begin_frame */
+    uint32_t n_slices;
+    uint32_t failed;      /* 1: the frame was invalidated and carries no times */
+    const uint32_t *tags; /* n_slices tags, valid until the next collect */
+    const float *micros;  /* n_slices durations in microseconds */
+} bl_frame_timing;
+
+typedef struct {
+    uint64_t frames_begun, frames_timed, frames_skipped, frames_failed, frames_dropped;
+} bl_timer_stats_t;
+
+int bl_timer_create(bl_ctx *ctx, uint32_t max_slices, bl_timer **out);
+void bl_timer_destroy(bl_timer *timer);
+/* Opens a frame. `*timed` is 0 when its ring slot is still in flight: the
+ * frame then runs untimed and counts as skipped (FrameTimestamps::is_timed). */
+int bl_timer_begin_frame(bl_timer *timer, uint64_t frame, uint32_t *timed);
+/* Closes the open frame; `*resolved` names it for bl_timer_submitted. */
+int bl_timer_resolve(bl_timer *timer, uint32_t *resolved);
+/* The host says the frame's work reached the stream. A resolved frame never
+ * submitted is dropped by the next begin_frame, unread. */
+int bl_timer_submitted(bl_timer *timer, uint32_t resolved);
+/* The frames whose events have all completed, in submission order, without
+ * blocking (hipEventQuery). Fills up to `cap` entries. */
+int bl_timer_collect(bl_timer *timer, bl_frame_timing *out, uint32_t cap,
+                     uint32_t *n_out);
+/* Every submitted frame not yet collected is marked failed (never decoded). */
+int bl_timer_invalidate_submitted(bl_timer *timer);
+int bl_timer_stats(const bl_timer *timer, bl_timer_stats_t *out);
+
+/* ---- a fixed amount of GPU time (a synthetic render load) ---- */
+/* Launches one kernel on the context's stream that spins every CU for
+ * `micros` microseconds of the device's constant-rate wall clock. */
+int bl_spin(bl_ctx *ctx, uint32_t micros);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,307 @@
+"""The oracle: ctypes wrapper of oracle/build/liboracle.so.
+
+TEST INFRASTRUCTURE ONLY. tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it as the checker (or, for the CPU baseline, as the
+reference path timed on the host). The product library never imports it.
+
+`ref_*` are the reference's f64 CPU reference ops
+(crates/beatlm-bench/src/reference.rs); `wg_*` the reference's WGSL kernels'
+f32 arithmetic in their order (crates/beatlm/src/codegen/wgsl.rs).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB = HERE / "build" / "liboracle.so"
+
+# reference.rs:22-24
+TOLERANCE_ABS = 1e-4
+TOLERANCE_REL = 1e-4
+
+_lib = None
+_F = C.POINTER(C.c_float)
+_S = C.c_size_t
+
+
+class BlockWeights(C.Structure):
+    _fields_ = [
+        (n, _F)
+        for n in (
+            "norm1_g", "norm1_b", "qkv_w", "qkv_b", "proj_w", "proj_b", "ls1",
+            "norm2_g", "norm2_b", "fc1_w", "fc1_b", "fc2_w", "fc2_b", "ls2",
+        )
+    ]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+        h = C.CDLL(str(LIB))
+        sig = {
+            "blo_uniform": [C.c_uint64, _S, C.c_float, C.c_float, _F],
+            "blo_normal": [C.c_uint64, _S, C.c_float, C.c_float, _F],
+            "blo_ref_layernorm": [_F, _F, _F, _S, _S, C.c_float, _F],
+            "blo_ref_matmul": [_F, _F, _F, _S, _S, _S, _F],
+            "blo_ref_add": [_F, _F, _S, _F],
+            "blo_ref_relu": [_F, _S, _F],
+            "blo_ref_gelu_tanh": [_F, _S, _F],
+            "blo_ref_scale": [_F, _S, C.c_float, _F],
+            "blo_ref_gelu_erf": [_F, _S, _F],
+            "blo_ref_channel_scale": [_F, _F, _S, _S, _F],
+            "blo_ref_attention_scores": [_F, _S, _S, _S, _F],
+            "blo_ref_softmax": [_F, _S, _S, _F],
+            "blo_ref_attention_values": [_F, _F, _S, _S, _S, _F],
+            "blo_ref_attention": [_F, _S, _S, _S, C.c_float, _F],
+            "blo_ref_patch_embed": [_F, _F, _F, _S, _S, _S, _S, _S, _F],
+            "blo_ref_prepend_token": [_F, _F, _S, _S, _F],
+            "blo_ref_vit_block": [_F, C.POINTER(BlockWeights), _S, _S, _S, _S, C.c_float, C.c_int, _F],
+            "blo_wg_layernorm": [_F, _F, _F, _S, _S, C.c_float, _F],
+            "blo_wg_softmax": [_F, _S, _S, _F],
+            "blo_wg_matmul": [_F, _F, _F, _S, _S, _S, _F],
+            "blo_wg_block_scratch_floats": [_S, _S, _S, _S],
+            "blo_wg_vit_block": [_F, C.POINTER(BlockWeights), _S, _S, _S, _S, C.c_float, C.c_int, _F, _F],
+        }
+        for name, args in sig.items():
+            getattr(h, name).argtypes = args
+            getattr(h, name).restype = None
+        h.blo_erf.argtypes = [C.c_double]
+        h.blo_erf.restype = C.c_double
+        h.blo_wg_gelu_erf1.argtypes = [C.c_float]
+        h.blo_wg_gelu_erf1.restype = C.c_float
+        h.blo_wg_block_scratch_floats.restype = C.c_size_t
+        _lib = h
+    return _lib
+
+
+def _p(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], "oracle arrays are contiguous f32"
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---- generators ----
+
+def uniform(seed: int, count: int, low: float, high: float) -> np.ndarray:
+    out = np.empty(count, np.float32)
+    lib().blo_uniform(seed, count, low, high, _p(out))
+    return out
+
+
+def normal(seed: int, count: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(count, np.float32)
+    lib().blo_normal(seed, count, mean, std, _p(out))
+    return out
+
+
+def fan_in_weights(seed: int, count: int, fan_in: int) -> np.ndarray:
+    """U(+-1/sqrt(fan_in)), the reference's test weights (harness.rs:80-84)."""
+    s = np.float32(1.0) / np.sqrt(np.float32(fan_in))
+    return uniform(seed, count, -s, s)
+
+
+def xavier(seed: int, fan_in: int, fan_out: int) -> np.ndarray:
+    """Xavier-uniform U(+-sqrt(6 / (fan_in + fan_out)))."""
+    a = float(np.sqrt(6.0 / (fan_in + fan_out)))
+    return uniform(seed, fan_in * fan_out, -a, a)
+
+
+# ---- f64 reference ops ----
+
+def erf(x: float) -> float:
+    return float(lib().blo_erf(x))
+
+
+def layernorm(x, gamma, beta, rows, c, eps):
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    out = np.empty(rows * c, np.float32)
+    lib().blo_ref_layernorm(_p(x), _p(gamma), _p(beta), rows, c, eps, _p(out))
+    return out
+
+
+def matmul(a, b, bias, m, k, n):
+    a, b = _f32(a), _f32(b)
+    keep = _f32(bias) if bias is not None else None
+    out = np.empty(m * n, np.float32)
+    lib().blo_ref_matmul(_p(a), _p(b), _p(keep) if keep is not None else None, m, k, n, _p(out))
+    return out
+
+
+def add(a, b):
+    a, b = _f32(a), _f32(b)
+    out = np.empty(a.size, np.float32)
+    lib().blo_ref_add(_p(a), _p(b), a.size, _p(out))
+    return out
+
+
+def relu(x):
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib().blo_ref_relu(_p(x), x.size, _p(out))
+    return out
+
+
+def gelu_tanh(x):
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib().blo_ref_gelu_tanh(_p(x), x.size, _p(out))
+    return out
+
+
+def scale(x, f):
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib().blo_ref_scale(_p(x), x.size, f, _p(out))
+    return out
+
+
+def gelu_erf(x):
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib().blo_ref_gelu_erf(_p(x), x.size, _p(out))
+    return out
+
+
+def channel_scale(x, s):
+    x, s = _f32(x), _f32(s)
+    out = np.empty(x.size, np.float32)
+    lib().blo_ref_channel_scale(_p(x), _p(s), x.size, s.size, _p(out))
+    return out
+
+
+def attention_scores(qkv, t, h, d):
+    qkv = _f32(qkv)
+    out = np.empty(t * h * t, np.float32)
+    lib().blo_ref_attention_scores(_p(qkv), t, h, d, _p(out))
+    return out
+
+
+def softmax(x, cols):
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib().blo_ref_softmax(_p(x), x.size // cols, cols, _p(out))
+    return out
+
+
+def attention_values(probs, qkv, t, h, d):
+    probs, qkv = _f32(probs), _f32(qkv)
+    out = np.empty(t * h * d, np.float32)
+    lib().blo_ref_attention_values(_p(probs), _p(qkv), t, h, d, _p(out))
+    return out
+
+
+def attention(qkv, t, h, d, scale_factor):
+    qkv = _f32(qkv)
+    out = np.empty(t * h * d, np.float32)
+    lib().blo_ref_attention(_p(qkv), t, h, d, scale_factor, _p(out))
+    return out
+
+
+def patch_embed(image, w, bias, gh, gw, p, cin, cout):
+    image, w = _f32(image), _f32(w)
+    out = np.empty(gh * gw * cout, np.float32)
+    keep = _f32(bias) if bias is not None else None
+    lib().blo_ref_patch_embed(_p(image), _p(w), _p(keep) if keep is not None else None, gh, gw, p, cin, cout, _p(out))
+    return out
+
+
+def prepend_token(token, tokens, rows, c):
+    token, tokens = _f32(token), _f32(tokens)
+    out = np.empty((rows + 1) * c, np.float32)
+    lib().blo_ref_prepend_token(_p(token), _p(tokens), rows, c, _p(out))
+    return out
+
+
+def _weights_struct(w: dict):
+    arrays = {k: _f32(v) for k, v in w.items()}
+    s = BlockWeights(**{k: _p(v) for k, v in arrays.items()})
+    return s, arrays
+
+
+def vit_block(x, w: dict, t, h, d, mlp, eps, attention_rounded=True):
+    x = _f32(x)
+    s, keep = _weights_struct(w)
+    out = np.empty(t * h * d, np.float32)
+    lib().blo_ref_vit_block(_p(x), C.byref(s), t, h, d, mlp, eps, 1 if attention_rounded else 0, _p(out))
+    del keep
+    return out
+
+
+# ---- WGSL-order emulation ----
+
+def wg_gelu_erf(x):
+    return np.array([lib().blo_wg_gelu_erf1(float(v)) for v in np.asarray(x, np.float32)], np.float32)
+
+
+def wg_layernorm(x, gamma, beta, rows, c, eps):
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    out = np.empty(rows * c, np.float32)
+    lib().blo_wg_layernorm(_p(x), _p(gamma), _p(beta), rows, c, eps, _p(out))
+    return out
+
+
+def wg_softmax(x, cols):
+    x = _f32(x)
+    out = np.empty(x.size, np.float32)
+    lib().blo_wg_softmax(_p(x), x.size // cols, cols, _p(out))
+    return out
+
+
+def wg_matmul(a, b, bias, m, k, n):
+    a, b = _f32(a), _f32(b)
+    keep = _f32(bias) if bias is not None else None
+    out = np.empty(m * n, np.float32)
+    lib().blo_wg_matmul(_p(a), _p(b), _p(keep) if keep is not None else None, m, k, n, _p(out))
+    return out
+
+
+class WgBlock:
+    """The reference's 9 fused kernels of one block on the host, with its
+    scratch allocated once so repeated runs time only the arithmetic."""
+
+    def __init__(self, w: dict, t, h, d, mlp, eps, threads=0):
+        self.s, self.keep = _weights_struct(w)
+        self.t, self.h, self.d, self.mlp, self.eps, self.threads = t, h, d, mlp, eps, threads
+        n = lib().blo_wg_block_scratch_floats(t, h, d, mlp)
+        self.scratch = np.empty(n, np.float32)
+
+    def __call__(self, x):
+        x = _f32(x)
+        out = np.empty(self.t * self.h * self.d, np.float32)
+        lib().blo_wg_vit_block(
+            _p(x), C.byref(self.s), self.t, self.h, self.d, self.mlp, self.eps, self.threads,
+            _p(self.scratch), _p(out),
+        )
+        return out
+
+
+def within_tolerance(got, want, abs_tol=TOLERANCE_ABS, rel_tol=TOLERANCE_REL) -> np.ndarray:
+    """reference.rs:629-632; false for a NaN on either side."""
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    with np.errstate(invalid="ignore"):
+        return np.abs(got - want) <= abs_tol + rel_tol * np.abs(want)
+
+
+def first_mismatch(got, want, abs_tol=TOLERANCE_ABS, rel_tol=TOLERANCE_REL):
+    """reference.rs:635-645: (index, got, want) of the first element outside
+    the tolerance, or None."""
+    got = np.asarray(got, np.float32).ravel()
+    want = np.asarray(want, np.float32).ravel()
+    if got.size != want.size:
+        return (min(got.size, want.size), float("nan"), float("nan"))
+    bad = np.flatnonzero(~within_tolerance(got, want, abs_tol, rel_tol))
+    if bad.size == 0:
+        return None
+    i = int(bad[0])
+    return (i, float(got[i]), float(want[i]))

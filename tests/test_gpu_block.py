@@ -1,0 +1,83 @@
+"""One complete pre-norm encoder block on the GPU against the oracle's forward
+pass (reference.rs:520-544), fused (flash attention), fused with the
+reference's three attention kernels, unfused and split — the reference's
+vit.rs:240-309 — plus the f16 configurations and a 12-block encoder."""
+
+import numpy as np
+import pytest
+
+import oracle
+from beatlm_amd import hip, ir
+from tests.blockdata import block_graph, block_values, block_weights, max_abs_err
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+def assert_close(got, want, what):
+    bad = oracle.first_mismatch(got, want)
+    assert bad is None, f"{what}: element {bad[0]} is {bad[1]}, the oracle says {bad[2]}; max abs error {max_abs_err(got, want):.3e}"
+
+
+@pytest.fixture(scope="module")
+def small_block():
+    t, d, h, mlp = 1370, 384, 6, 1536
+    x = oracle.uniform(20, t * d, -2.0, 2.0)
+    w = block_weights(d, mlp, 100, "reference")
+    want = oracle.vit_block(x, w, t, h, d // h, mlp, EPS)
+    return (t, d, h, mlp), x, w, want
+
+
+@pytest.mark.parametrize(
+    "fusion,parts,flash",
+    [
+        (ir.FUSION_ON, 1, True),
+        (ir.FUSION_ON, 1, False),
+        (ir.FUSION_OFF, 1, False),
+        (ir.FUSION_ON, 3, True),
+        (ir.FUSION_ON, 22, True),
+        (ir.FUSION_ON, 3, False),
+    ],
+)
+def test_one_encoder_block_with_random_weights_matches_the_oracle_block(ctx, small_block, fusion, parts, flash):
+    (t, d, h, mlp), x, w, want = small_block
+    g, ids = block_graph(t, d, h, mlp, EPS)
+    got = ir.run_on_gpu(ctx, g, block_values(ids, x, w), fusion, parts, flash)[ids.output]
+    assert_close(got, want, f"encoder block, fusion {fusion}, {parts} parts, flash {flash}")
+
+
+def test_the_block_in_f32_matrix_core_math_matches_the_oracle(ctx, small_block):
+    (t, d, h, mlp), x, w, want = small_block
+    ctx.set_f32_math(hip.F32_MATH_MFMA_F32)
+    try:
+        g, ids = block_graph(t, d, h, mlp, EPS)
+        got = ir.run_on_gpu(ctx, g, block_values(ids, x, w))[ids.output]
+        assert_close(got, want, "encoder block, v_mfma_f32")
+    finally:
+        ctx.set_f32_math(hip.F32_MATH_SPLIT_BF16)
+
+
+def test_the_benchmark_block_with_xavier_weights_and_normal_activations(ctx):
+    t, d, h, mlp = 257, 384, 6, 1536
+    x = oracle.normal(7, t * d)
+    w = block_weights(d, mlp, 300, "xavier")
+    want = oracle.vit_block(x, w, t, h, d // h, mlp, EPS)
+    g, ids = block_graph(t, d, h, mlp, EPS)
+    got = ir.run_on_gpu(ctx, g, block_values(ids, x, w))[ids.output]
+    assert_close(got, want, "ViT-S block, 257 tokens")
+
+
+@pytest.mark.parametrize("t,d,h", [(1370, 768, 12), (1370, 1024, 16), (5477, 384, 6)])
+def test_the_f16_block_is_within_its_tolerance(ctx, t, d, h):
+    mlp = 4 * d
+    x = oracle.normal(9, t * d).astype(np.float16)
+    w = {k: v.astype(np.float16) for k, v in block_weights(d, mlp, 500, "xavier").items()}
+    want = oracle.vit_block(
+        x.astype(np.float32), {k: v.astype(np.float32) for k, v in w.items()}, t, h, d // h, mlp, EPS,
+        attention_rounded=False,
+    )
+    g, ids = block_graph(t, d, h, mlp, EPS)
+    got = ir.run_on_gpu(ctx, g, block_values(ids, x, w), dtype=hip.F16)[ids.output]
+    err = max_abs_err(got, want)
+    assert err <= 2e-2, f"f16 block t={t} d={d}: max abs error {err:.3e}"
