@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -62,6 +63,8 @@ struct bl_arenas {
     char *base = nullptr;
     std::vector<uint64_t> offset, size;
     uint64_t total = 0;
+    // Bumped by every host write: packed copies of weights made before it are stale.
+    uint64_t generation = 1;
 };
 
 // ---- context ----
@@ -233,6 +236,7 @@ extern "C" int bl_arenas_write(bl_arenas *a, uint32_t arena, uint64_t offset, co
     hipError_t e = hipMemcpyAsync(a->base + a->offset[arena] + offset, src, bytes, hipMemcpyHostToDevice,
                                   a->ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(a->ctx->stream);
+    a->generation++;
     return e == hipSuccess ? BL_OK : hip_fail(a->ctx, e, "arena write");
 }
 
@@ -264,6 +268,7 @@ struct Launch {
     Family family;
     Math math = Math::F32;
     int tile = 0;
+    int pack = -1;  // the packed B a GEMM reads
     bool f16 = false;
     Gather gather = Gather::SCORES;
     PerElement element = PerElement::MAP;
@@ -278,6 +283,20 @@ struct Launch {
 struct Kernel {
     std::string label;
     std::vector<Launch> per_set;
+};
+
+// A packed copy of one B operand (a weight matrix), remade when the host has
+// written the arenas since, or before every launch when a kernel of the
+// program writes the bytes it is packed from.
+struct Pack {
+    Math math;
+    const void *src;
+    uint32_t arena;
+    uint64_t offset, size;
+    uint32_t k, n, k_pad, n_pad;
+    uint64_t dst_offset;  // into the kernels' pack buffer
+    uint64_t generation = 0;
+    bool dynamic = false;
 };
 
 const char *main_name(uint32_t m) {
@@ -410,6 +429,8 @@ struct bl_kernels {
     std::vector<Kernel> kernels;
     uint32_t sets = 1;
     void *scratch = nullptr;
+    std::vector<Pack> packs;
+    void *pack_buffer = nullptr;
 };
 
 extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs, uint32_t n,
@@ -552,17 +573,84 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
                 L.ln = LayerNormArgs{rd(0), rd(1), rd(2), out_ptr, d[0], d[1], pt.start, pt.end, s.epsilon, epi};
                 variant = "wave-per-row";
                 break;
-            case BL_MAIN_MATMUL: {
+            case BL_MAIN_MATMUL:
+            case BL_MAIN_PATCH_EMBED: {
                 L.family = Family::GEMM;
-                L.gemm = GemmArgs{rd(0), rd(1), d[3] ? rd(2) : nullptr, out_ptr, d[0], d[2], d[1], pt.start, pt.end, epi};
-                // The largest tile that still gives every CU a workgroup.
+                const bool patch = s.main == BL_MAIN_PATCH_EMBED;
+                const uint32_t gm = patch ? d[0] * d[1] : d[0];
+                const uint32_t gk = patch ? d[2] * d[2] * d[3] : d[1];
+                const uint32_t gn = patch ? d[4] : d[2];
+                const bool has_bias = patch ? d[5] != 0 : d[3] != 0;
+                GemmArgs ga{};
+                ga.a = rd(0);
+                ga.bias = has_bias ? rd(2) : nullptr;
+                ga.c = out_ptr;
+                ga.m = gm;
+                ga.n = gn;
+                ga.k = gk;
+                ga.k_pad = (gk + PACK_K - 1) / PACK_K * PACK_K;
+                ga.n_pad = (gn + PACK_N - 1) / PACK_N * PACK_N;
+                ga.row0 = pt.start;
+                ga.row1 = pt.end;
+                ga.load = patch ? 2 : 0;
+                ga.pipeline = getenv("BL_GEMM_NO_PIPELINE") ? 0 : 1;
+                if (patch) {
+                    ga.p0 = d[1];
+                    ga.p1 = d[2];
+                    ga.p2 = d[3];
+                    ga.p3 = d[1] * d[2];
+                }
+                ga.epi = epi;
+                // Epilogues with a kernel of their own: GELU (erf); LayerScale over the
+                // output's columns followed by the residual add; anything else runs the
+                // steps in order.
+                if (s.n_epilogue == 0) ga.epi_mode = 0;
+                else if (s.n_epilogue == 1 && s.epilogue[0].kind == BL_EPI_GELU_ERF) ga.epi_mode = 1;
+                else if (s.n_epilogue == 2 && s.epilogue[0].kind == BL_EPI_CHANNEL_SCALE &&
+                         s.epilogue[0].channels == gn && s.epilogue[1].kind == BL_EPI_ADD) ga.epi_mode = 2;
+                else ga.epi_mode = 3;
+                // The packed B: one per distinct weight placement and math.
+                const bl_binding &bb = s.bindings[s.reads[1]];
+                uint32_t barena = bb.arena;
+                uint64_t boff = bb.offset;
+                for (uint32_t t = 0; t < sets[si].count; t++)
+                    if (sets[si].items[t].original == bb.tensor) {
+                        barena = sets[si].items[t].arena;
+                        boff = sets[si].items[t].offset;
+                    }
+                int pack = -1;
+                for (size_t q = 0; q < ks->packs.size(); q++) {
+                    const Pack &pk = ks->packs[q];
+                    if (pk.arena == barena && pk.offset == boff && pk.math == fmath && pk.k == gk && pk.n == gn) pack = (int)q;
+                }
+                if (pack < 0) {
+                    Pack pk{};
+                    pk.math = fmath;
+                    pk.src = rd(1);
+                    pk.arena = barena;
+                    pk.offset = boff;
+                    pk.size = bb.size;
+                    pk.k = gk;
+                    pk.n = gn;
+                    pk.k_pad = ga.k_pad;
+                    pk.n_pad = ga.n_pad;
+                    ks->packs.push_back(pk);
+                    pack = (int)ks->packs.size() - 1;
+                }
+                L.pack = pack;
+                L.gemm = ga;
+                // The largest tile that still gives every CU two workgroups.
                 const uint32_t rows = pt.end - pt.start;
-                const int order[] = {TILE_128x128, TILE_64x128, TILE_128x64, TILE_64x64, TILE_32x64};
+                const int order[] = {TILE_128x64, TILE_64x128, TILE_64x64, TILE_32x64};
                 int chosen = TILE_32x64;
                 for (int t : order) {
                     uint64_t wgs = (uint64_t)((rows + gemm_tile_rows(t) - 1) / gemm_tile_rows(t)) *
-                                   ((d[2] + gemm_tile_cols(t) - 1) / gemm_tile_cols(t));
-                    if (wgs >= ctx->compute_units) { chosen = t; break; }
+                                   ((gn + gemm_tile_cols(t) - 1) / gemm_tile_cols(t));
+                    if (wgs >= 2ull * ctx->compute_units) { chosen = t; break; }
+                }
+                if (const char *force = getenv("BL_GEMM_TILE")) {
+                    int t = atoi(force);
+                    if (t >= 0 && t < TILE_COUNT) chosen = t;
                 }
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
@@ -579,13 +667,6 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
                 L.family = Family::GATHER;
                 L.gather = Gather::VALUES;
                 L.ga = GatherArgs{rd(0), rd(1), nullptr, out_ptr, d[2], d[0], d[1], pt.start, pt.end, d[0], d[1], d[2], 0, epi};
-                variant = "valu-tiled";
-                break;
-            case BL_MAIN_PATCH_EMBED:
-                L.family = Family::GATHER;
-                L.gather = Gather::PATCH;
-                L.ga = GatherArgs{rd(0), rd(1), d[5] ? rd(2) : nullptr, out_ptr, d[4], d[2] * d[2] * d[3], 1,
-                                  pt.start, pt.end, d[1], d[2], d[3], d[1] * d[2], epi};
                 variant = "valu-tiled";
                 break;
             case BL_MAIN_SOFTMAX:
@@ -616,16 +697,16 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
                 L.family = Family::FLASH;
                 const uint32_t rows = pt.end - pt.start;
                 const uint32_t wgs = (rows + FLASH_ROWS - 1) / FLASH_ROWS * d[1];
-                const uint32_t ntiles = (d[0] + 63) / 64;
+                const uint32_t t_pad = (d[0] + 63) / 64 * 64;
+                const uint32_t ntiles = t_pad / 64;
                 // Enough workgroups for two per CU, each split keeping two key tiles or more.
                 uint32_t splits = (2 * ctx->compute_units + wgs - 1) / wgs;
-                splits = std::max<uint32_t>(1, std::min<uint32_t>(splits, ntiles / 2));
-                L.fl = FlashArgs{rd(0), out_ptr, nullptr, nullptr, d[0], d[1], pt.start, pt.end, splits, s.scale};
-                if (splits > 1) {
-                    uint64_t need_bytes = (uint64_t)splits * d[0] * d[1] * (FLASH_HEAD_DIM + 2) * sizeof(float);
-                    scratch_bytes = std::max(scratch_bytes, need_bytes);
-                    flash_users.push_back({ki, si});
-                }
+                splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, ntiles / 2, FLASH_MAX_SPLITS}));
+                L.fl = FlashArgs{rd(0), out_ptr, nullptr, nullptr, nullptr, nullptr, d[0], d[1], t_pad, pt.start, pt.end, splits, s.scale};
+                uint64_t need_bytes = flash_operand_bytes(fmath, d[1], t_pad);
+                if (splits > 1) need_bytes += (uint64_t)splits * d[0] * d[1] * (FLASH_HEAD_DIM + 2) * sizeof(float);
+                scratch_bytes = std::max(scratch_bytes, need_bytes);
+                flash_users.push_back({ki, si});
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
                           " splits=" + std::to_string(splits);
                 break;
@@ -636,13 +717,38 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
         }
         ks->kernels.push_back(std::move(k));
     }
+    if (!ks->packs.empty()) {
+        uint64_t total = 0;
+        for (Pack &pk : ks->packs) {
+            pk.dst_offset = total;
+            total += (packed_bytes(pk.math, pk.k_pad, pk.n_pad) + 255) / 256 * 256;
+            // Written by a kernel of this program: packed again before every launch.
+            for (uint32_t ki = 0; ki < n && !pk.dynamic; ki++) {
+                const bl_binding &o = specs[ki].bindings[specs[ki].n_bindings - 1];
+                if (o.arena == pk.arena && o.offset < pk.offset + pk.size && pk.offset < o.offset + o.size)
+                    pk.dynamic = true;
+            }
+        }
+        ks->pack_buffer = bl_device_alloc(ctx, total);
+        if (!ks->pack_buffer) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of packed weights", (unsigned long long)total);
+        for (Kernel &k : ks->kernels)
+            for (Launch &L : k.per_set)
+                if (L.pack >= 0) L.gemm.b = (char *)ks->pack_buffer + ks->packs[L.pack].dst_offset;
+    }
     if (scratch_bytes) {
         ks->scratch = bl_device_alloc(ctx, scratch_bytes);
         if (!ks->scratch) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
+        // Kernels run one after another on the stream, so every flash kernel
+        // uses the same scratch: operands, then partial outputs and statistics.
         for (auto [ki, si] : flash_users) {
             FlashArgs &f = ks->kernels[ki].per_set[si].fl;
-            f.partial = (float *)ks->scratch;
-            f.stats = (float *)ks->scratch + (uint64_t)f.splits * f.tokens * f.heads * FLASH_HEAD_DIM;
+            const Math fm = ks->kernels[ki].per_set[si].math;
+            const uint64_t operands = flash_operand_bytes(fm, f.heads, f.t_pad);
+            char *base = (char *)ks->scratch;
+            f.kp = base;
+            f.vt = base + operands / 2;
+            f.partial = (float *)(base + operands);
+            f.stats = f.partial + (uint64_t)f.splits * f.tokens * f.heads * FLASH_HEAD_DIM;
         }
     }
     *out = ks;
@@ -651,11 +757,10 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
 
 extern "C" void bl_kernels_destroy(bl_kernels *k) {
     if (!k) return;
-    if (k->scratch) {
-        hipSetDevice(k->ctx->device);
-        hipStreamSynchronize(k->ctx->stream);
-        hipFree(k->scratch);
-    }
+    hipSetDevice(k->ctx->device);
+    hipStreamSynchronize(k->ctx->stream);
+    if (k->scratch) hipFree(k->scratch);
+    if (k->pack_buffer) hipFree(k->pack_buffer);
     delete k;
 }
 
@@ -663,6 +768,16 @@ extern "C" uint32_t bl_kernels_len(const bl_kernels *k) { return k ? (uint32_t)k
 extern "C" uint32_t bl_kernels_sets(const bl_kernels *k) { return k ? k->sets : 0; }
 extern "C" const char *bl_kernels_label(const bl_kernels *k, uint32_t i) {
     return (k && i < k->kernels.size()) ? k->kernels[i].label.c_str() : nullptr;
+}
+
+// Packs a GEMM's B when its source may have changed since the last pack.
+static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
+    Pack &pk = k->packs[L.pack];
+    if (!pk.dynamic && pk.generation == k->arenas->generation) return hipSuccess;
+    PackArgs pa{pk.src, (char *)k->pack_buffer + pk.dst_offset, pk.k, pk.n, pk.k_pad, pk.n_pad};
+    hipError_t e = launch_pack(pa, pk.math, s);
+    if (e == hipSuccess) pk.generation = k->arenas->generation;
+    return e;
 }
 
 static hipError_t launch(const Launch &L, hipStream_t s) {
@@ -687,7 +802,9 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
         int r = bl_timer_slice_begin(timer, tag, s, &slice);
         if (r) return r;
     }
-    hipError_t e = launch(k->kernels[kernel].per_set[set], s);
+    const Launch &L = k->kernels[kernel].per_set[set];
+    hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
+    if (e == hipSuccess) e = launch(L, s);
     if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[kernel].label.c_str());
     if (timer && slice >= 0) bl_timer_slice_end(timer, slice, s);
     return BL_OK;
@@ -699,7 +816,9 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
         return fail(k->ctx, BL_ERR_NO_SUCH_KERNEL, "there is no kernel %u", first + count - 1);
     if (set >= k->sets) return fail(k->ctx, BL_ERR_NO_SUCH_SET, "there is no binding set %u", set);
     for (uint32_t i = first; i < first + count; i++) {
-        hipError_t e = launch(k->kernels[i].per_set[set], k->ctx->stream);
+        const Launch &L = k->kernels[i].per_set[set];
+        hipError_t e = L.pack >= 0 ? refresh_pack(k, L, k->ctx->stream) : hipSuccess;
+        if (e == hipSuccess) e = launch(L, k->ctx->stream);
         if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
     }
     return BL_OK;

@@ -101,4 +101,69 @@ __device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
     lo = (__bf16)(x - (float)hi);
 }
 
+
+// ---- direct HBM/L2 -> LDS staging (global_load_lds_dwordx4) ----
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt in [3:0] and
+// [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// The slot a chunk occupies in its staged row.
+//
+// LDS serves 64 banks of 4 bytes; a 16-byte read by 16 lanes is conflict-free
+// when their (row, slot) pairs cover 256 distinct bytes modulo 256. Rows of
+// 4 chunks (64 B) repeat every 4 rows, rows of 8 every 2, rows of 16 every
+// row, so the slot is XORed with the row bits above that period.
+template <int CPR>
+__device__ __forceinline__ int swz(int row, int chunk) {
+    if constexpr (CPR == 4) return chunk ^ ((row >> 2) & 3);
+    else if constexpr (CPR == 8) return chunk ^ ((row >> 1) & 7);
+    else return chunk ^ (row & 15);
+}
+
+// Issues one operand's direct loads for one stage: `rows` rows of CPR chunks,
+// the chunks spread over the 4 waves in lane order.
+// One operand's direct loads for one stage: ROWS rows of CPR 16-byte chunks,
+// spread over the 4 waves in lane order. The lane's byte offsets from the
+// operand's tile base (its row, clamped to `row_limit`, and its swizzled
+// chunk) are computed once; a stage then costs one address add per load.
+template <int ROWS, int CPR>
+struct RowLoader {
+    static constexpr int TOTAL = ROWS * CPR;
+    static constexpr int PER_WAVE = TOTAL / 4;
+    static constexpr int INSTR = (PER_WAVE + 63) / 64;
+    static_assert(TOTAL % 4 == 0, "chunks per wave");
+    uint32_t off[INSTR];
+    bool active[INSTR];
+    int wave;
+
+    __device__ __forceinline__ RowLoader(uint32_t row_stride_bytes, uint32_t row_limit, int wave_, int lane) : wave(wave_) {
+#pragma unroll
+        for (int q = 0; q < INSTR; q++) {
+            const int li = q * 64 + lane;
+            const int i = wave * PER_WAVE + li;
+            const int row = i / CPR, slot = i % CPR;
+            const uint32_t r = min((uint32_t)row, row_limit);
+            off[q] = r * row_stride_bytes + swz<CPR>(row, slot) * 16;
+            active[q] = li < PER_WAVE;
+        }
+    }
+    __device__ __forceinline__ void issue(const char *base, char *lds) const {
+#pragma unroll
+        for (int q = 0; q < INSTR; q++) {
+            if (active[q])
+                __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(base + off[q]),
+                                                 (__attribute__((address_space(3))) void *)(lds + (wave * PER_WAVE + q * 64) * 16),
+                                                 16, 0, 0);
+        }
+    }
+};
+
+template <int ROWS, int CPR>
+constexpr int loads_per_wave() { return ((ROWS * CPR / 4) + 63) / 64; }
+
 }  // namespace bl

@@ -622,7 +622,8 @@ extern "C" int bli_program_parts_within(const bli_program *p, const uint64_t *du
     if (n != p->kernels.size()) return err(BLI_ERR_PART_COUNTS, "%u entries given for a program of %zu kernels", n, p->kernels.size());
     if (bound == 0) return err(BLI_ERR_ZERO_BOUND, "a dispatch bound of zero cannot be met");
     for (uint32_t i = 0; i < n; i++) {
-        uint64_t wanted = std::max<uint64_t>((durations[i] + bound - 1) / bound, 1);
+        const uint64_t d = durations[i];
+        uint64_t wanted = std::max<uint64_t>(d / bound + (d % bound != 0), 1);
         parts_out[i] = (uint32_t)std::min<uint64_t>(wanted, std::max<uint32_t>(p->kernels[i].max_parts(), 1));
     }
     return 0;

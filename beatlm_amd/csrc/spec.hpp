@@ -36,11 +36,25 @@ struct LayerNormArgs {
 };
 
 struct GemmArgs {
-    const void *a, *b, *bias;
+    const void *a;
+    const void *b;        // the packed B: [planes][n_pad][k_pad]
+    const void *bias;
     void *c;
     uint32_t m, n, k;
+    uint32_t n_pad, k_pad;
     uint32_t row0, row1;
+    int load;             // A: 0 rows of whole vectors, 1 element by element, 2 patches of an image
+    int epi_mode;         // 0 none, 1 gelu_erf, 2 channel_scale(over n) + add, 3 any steps
+    int pipeline;         // 1: the LDS-ring kernel with direct loads (k a multiple of 32)
+    uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width
     EpilogueArgs epi;
+};
+
+// B [k][n] -> the GEMM's packed operand (transposed, padded, converted).
+struct PackArgs {
+    const void *src;
+    void *dst;
+    uint32_t k, n, k_pad, n_pad;
 };
 
 // The tiled products whose operands are gathered (the unfused attention
@@ -68,9 +82,11 @@ struct SoftmaxArgs {
 struct FlashArgs {
     const void *qkv;
     void *out;
+    void *kp;             // keys [planes][heads][t_pad][64] in the operand type
+    void *vt;             // values transposed [planes][heads][64][t_pad]
     float *partial;       // [splits][tokens][heads][64] f32, when splits > 1
     float *stats;         // [splits][tokens][heads][2] (max, sum), when splits > 1
-    uint32_t tokens, heads;
+    uint32_t tokens, heads, t_pad;
     uint32_t row0, row1;  // query rows of the part
     uint32_t splits;
     float scale;          // softmax scale (the Scale epilogue of the scores)
@@ -93,21 +109,36 @@ hipError_t launch_layernorm(const LayerNormArgs &a, bool f16, hipStream_t s);
 hipError_t launch_gemm_f32(const GemmArgs &a, int tile, hipStream_t s);
 hipError_t launch_gemm_split(const GemmArgs &a, int tile, hipStream_t s);
 hipError_t launch_gemm_f16(const GemmArgs &a, int tile, hipStream_t s);
+hipError_t launch_pack_f32(const PackArgs &a, hipStream_t s);
+hipError_t launch_pack_split(const PackArgs &a, hipStream_t s);
+hipError_t launch_pack_f16(const PackArgs &a, hipStream_t s);
 inline hipError_t launch_gemm(const GemmArgs &a, Math m, int tile, hipStream_t s) {
     if (a.row1 <= a.row0) return hipSuccess;
     return m == Math::F32 ? launch_gemm_f32(a, tile, s)
          : m == Math::SPLIT ? launch_gemm_split(a, tile, s) : launch_gemm_f16(a, tile, s);
 }
+inline hipError_t launch_pack(const PackArgs &a, Math m, hipStream_t s) {
+    return m == Math::F32 ? launch_pack_f32(a, s) : m == Math::SPLIT ? launch_pack_split(a, s) : launch_pack_f16(a, s);
+}
+// Bytes of a packed B.
+inline uint64_t packed_bytes(Math m, uint32_t k_pad, uint32_t n_pad) {
+    return (uint64_t)k_pad * n_pad * (m == Math::F16 ? 2 : 4);
+}
 hipError_t launch_gather(const GatherArgs &a, Gather g, bool f16, hipStream_t s);
 hipError_t launch_softmax(const SoftmaxArgs &a, bool f16, hipStream_t s);
 hipError_t launch_flash(const FlashArgs &a, Math m, hipStream_t s);
+uint64_t flash_operand_bytes(Math m, uint32_t heads, uint32_t t_pad);
+// The most key splits the merge takes.
+constexpr uint32_t FLASH_MAX_SPLITS = 8;
 hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s);
 hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
 
 // GEMM tile shapes the dispatcher can pick from: BM x BN.
-enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x128 = 3, TILE_128x64 = 4, TILE_COUNT = 5 };
-inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128}; return r[t]; }
-inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 128, 64}; return c[t]; }
+enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_COUNT = 4 };
+inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128}; return r[t]; }
+inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64}; return c[t]; }
+// K and N of a packed B are padded to these.
+constexpr uint32_t PACK_K = 32, PACK_N = 128;
 
 // The flash kernel's query rows per workgroup.
 constexpr uint32_t FLASH_ROWS = 64;

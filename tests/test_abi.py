@@ -1,0 +1,84 @@
+"""The C ABI as a drop-in boundary: the library loads without a GPU, exports
+every function include/beatlm_hip.h and include/beatlm_ir.h declare, and the
+structs the host bindings pass have the C layout (checked against gcc
+compiling the headers). CPU only; no compute call."""
+
+import ctypes as C
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from beatlm_amd import hip, ir
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADERS = [ROOT / "include" / "beatlm_hip.h", ROOT / "include" / "beatlm_ir.h"]
+
+
+def declared_functions(path):
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(bli?_[a-z0-9_]+)\s*\(", text)) - {"bl_timer_stats_t"})
+
+
+def test_the_library_exports_every_declared_function():
+    lib = hip.lib()
+    names = [n for h in HEADERS for n in declared_functions(h)]
+    assert len(names) > 50
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert missing == []
+
+
+def test_the_abi_version():
+    assert hip.lib().bl_abi_version() == 1
+
+
+C_LAYOUT = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "beatlm_ir.h"
+#define P(T) printf(#T " %zu\n", sizeof(T));
+#define O(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
+int main(void) {
+  P(bl_spec) O(bl_spec, part) O(bl_spec, n_reads) O(bl_spec, epilogue) O(bl_spec, bindings)
+  P(bl_binding) P(bl_epilogue) P(bl_part) P(bl_substitution) P(bl_binding_set)
+  P(bl_device_profile_t) O(bl_device_profile_t, compute_units) O(bl_device_profile_t, name)
+  P(bl_frame_timing) P(bl_timer_stats_t)
+  P(bli_op) P(bli_tensor_desc) P(bli_profile) P(bli_placement) P(bli_kernel_info)
+  O(bli_kernel_info, output_start) O(bli_kernel_info, bindings) P(bli_vit_dims) P(bli_block_ids) P(bli_embed_ids)
+  return 0;
+}
+"""
+
+
+def test_the_host_structs_have_the_c_layout(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(C_LAYOUT)
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines())
+    py = {
+        "bl_spec": hip.Spec, "bl_binding": hip.Binding, "bl_epilogue": hip.Epilogue, "bl_part": hip.Part,
+        "bl_substitution": hip.Substitution, "bl_binding_set": hip.BindingSet,
+        "bl_device_profile_t": hip.DeviceProfile, "bl_frame_timing": hip.FrameTiming,
+        "bl_timer_stats_t": hip.TimerStats, "bli_op": ir.Op, "bli_tensor_desc": ir.TensorDesc,
+        "bli_profile": ir.Profile, "bli_placement": ir.Placement, "bli_kernel_info": ir.KernelInfo,
+        "bli_vit_dims": ir.VitDims, "bli_block_ids": ir.BlockIds, "bli_embed_ids": ir.EmbedIds,
+    }
+    for name, cls in py.items():
+        assert int(got[name]) == C.sizeof(cls), name
+    for key, value in got.items():
+        if "." in key:
+            struct, field = key.split(".")
+            assert getattr(py[struct], field).offset == int(value), key
+
+
+def test_without_a_device_a_context_is_an_error_not_a_crash():
+    lib = hip.lib()
+    h = C.c_void_p()
+    rc = lib.bl_ctx_create(0, C.byref(h))
+    if rc == hip.OK:
+        lib.bl_ctx_destroy(h)
+        pytest.skip("a GPU is visible")
+    assert rc in (hip.ERR_HIP, hip.ERR_INVALID_ARGUMENT)
+    assert lib.bl_ctx_create(-1, C.byref(h)) != hip.OK
