@@ -43,6 +43,7 @@ SOURCES = [
     "backend.cpp",
     "timer.cpp",
     "ir.cpp",
+    "schedule.cpp",
 ]
 
 

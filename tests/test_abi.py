@@ -1,5 +1,6 @@
 """The C ABI as a drop-in boundary: the library loads without a GPU, exports
-every function include/beatlm_hip.h and include/beatlm_ir.h declare, and the
+every function include/beatlm_hip.h, include/beatlm_ir.h and
+include/beatlm_schedule.h declare, and the
 structs the host bindings pass have the C layout (checked against gcc
 compiling the headers). CPU only; no compute call."""
 
@@ -10,15 +11,15 @@ import subprocess
 
 import pytest
 
-from beatlm_amd import hip, ir
+from beatlm_amd import hip, ir, schedule
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADERS = [ROOT / "include" / "beatlm_hip.h", ROOT / "include" / "beatlm_ir.h"]
+HEADERS = [ROOT / "include" / "beatlm_hip.h", ROOT / "include" / "beatlm_ir.h", ROOT / "include" / "beatlm_schedule.h"]
 
 
 def declared_functions(path):
     text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(bli?_[a-z0-9_]+)\s*\(", text)) - {"bl_timer_stats_t"})
+    return sorted(set(re.findall(r"\b(bl[is]?_[a-z0-9_]+)\s*\(", text)) - {"bl_timer_stats_t"})
 
 
 def test_the_library_exports_every_declared_function():
@@ -37,6 +38,7 @@ C_LAYOUT = r"""
 #include <stddef.h>
 #include <stdio.h>
 #include "beatlm_ir.h"
+#include "beatlm_schedule.h"
 #define P(T) printf(#T " %zu\n", sizeof(T));
 #define O(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
 int main(void) {
@@ -46,6 +48,7 @@ int main(void) {
   P(bl_frame_timing) P(bl_timer_stats_t)
   P(bli_op) P(bli_tensor_desc) P(bli_profile) P(bli_placement) P(bli_kernel_info)
   O(bli_kernel_info, output_start) O(bli_kernel_info, bindings) P(bli_vit_dims) P(bli_block_ids) P(bli_embed_ids)
+  P(bls_frame) P(bls_frame_plan) O(bls_frame_plan, runs) O(bls_frame_plan, budget)
   return 0;
 }
 """
@@ -64,6 +67,7 @@ def test_the_host_structs_have_the_c_layout(tmp_path):
         "bl_timer_stats_t": hip.TimerStats, "bli_op": ir.Op, "bli_tensor_desc": ir.TensorDesc,
         "bli_profile": ir.Profile, "bli_placement": ir.Placement, "bli_kernel_info": ir.KernelInfo,
         "bli_vit_dims": ir.VitDims, "bli_block_ids": ir.BlockIds, "bli_embed_ids": ir.EmbedIds,
+        "bls_frame": schedule.Frame, "bls_frame_plan": schedule._Plan,
     }
     for name, cls in py.items():
         assert int(got[name]) == C.sizeof(cls), name
