@@ -420,6 +420,12 @@ def prepare(
         program = program.fuse_attention()
     if parts != 1:
         program = program.split([parts] * len(program))
+    return realise(ctx, program, dtype)
+
+
+def realise(ctx: hip.Context, program: Program, dtype: int = hip.F32) -> Prepared:
+    """Plan `program` against the MI355X profile in `dtype` storage, allocate
+    its arenas and build its kernels."""
     program.set_dtype(dtype)
     plan = Plan(program.tensors(), profile("mi355x"))
     arenas = hip.Arenas(ctx, plan.arenas())

@@ -11,7 +11,13 @@ over its 12 blocks (the patch embedding's time is counted in, conservatively).
 Prints ONE JSON line. Everything is timed with inputs resident in HBM.
 
   python bench.py [--steps K] [--warmup W] [--config vit-s-518|vit-s-224|vit-b-518|vit-l-518x4|vit-s-1036]
-                  [--f32-math split|mfma] [--no-cpu-baseline] [--graph]
+                  [--f32-math split|mfma] [--no-cpu-baseline] [--frame-loop-frames N]
+
+The same line carries `frame_loop`: the high-resolution encoder (ViT-S/14 at
+1036 x 1036, 5477 tokens, 12 blocks, f16) run as frame-budget slices at 60
+frames per second beside a render load spinning the GPU for 8 ms a frame,
+after calibration: slices per frame, the delivery latency k the calibrated
+costs call for, deliveries and misses (--frame-loop-frames 0 skips it).
 """
 
 from __future__ import annotations
@@ -28,7 +34,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from beatlm_amd import hip, ir  # noqa: E402
+from beatlm_amd import frameloop, hip, ir  # noqa: E402
 
 METRIC = "µs per ViT encoder block + attention TFLOP/s (% MFMA peak), 1 MI355X"
 
@@ -193,6 +199,9 @@ def main() -> int:
     ap.add_argument("--f32-math", default="split", choices=["split", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-frames", type=int, default=20)
+    ap.add_argument("--frame-loop-frames", type=int, default=120)
+    ap.add_argument("--render-us", type=int, default=8000)
+    ap.add_argument("--max-dispatch-us", type=int, default=frameloop.DEFAULT_MAX_DISPATCH_US)
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -303,6 +312,16 @@ def main() -> int:
     if attn:
         result["attention_tflops"] = attn["achieved"]
         result["attention_frac_of_mfma_peak"] = attn["frac"]
+
+    if args.frame_loop_frames > 0:
+        hi = CONFIGS["vit-s-1036"]
+        g5, emb5, ids5, tokens5 = build_encoder(hi)
+        vals5 = synthetic_values(hi, emb5, ids5, tokens5, np.float16)
+        loop = frameloop.run(ctx, g5, vals5, ids5[-1].output, hip.F16, frames=args.frame_loop_frames,
+                             render_us=args.render_us, bound_us=args.max_dispatch_us)
+        loop["workload"] = (f"vit-s-1036: patch embed + {hi['blocks']} pre-LN ViT blocks, {tokens5} tokens, "
+                            f"width 384, 6 heads x 64, f16, as " + loop["workload"])
+        result["frame_loop"] = loop
 
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)

@@ -1,0 +1,186 @@
+"""The slice timer (hipEvent pairs, crates/beatlm/src/gpu/timer.rs:185-464 and
+its tests), the fixed-time render load, and the frame-budget loop of the
+high-resolution encoder (calibrate -> parts_within -> split -> scheduled
+slices), on a small block so each test takes seconds."""
+
+import time
+
+import pytest
+
+import oracle
+from beatlm_amd import frameloop, hip, ir
+from tests.blockdata import block_graph, block_values, block_weights
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+
+
+@pytest.fixture(scope="module")
+def small(ctx):
+    t, d, h, mlp = 257, 384, 6, 1536
+    x = oracle.uniform(31, t * d, -2.0, 2.0)
+    w = block_weights(d, mlp, 100, "reference")
+    g, ids = block_graph(t, d, h, mlp, EPS)
+    vals = block_values(ids, x, w)
+    prep = ir.prepare(ctx, g)
+    for tid, v in vals.items():
+        prep.write(tid, v)
+    yield g, ids, vals, prep
+    prep.kernels.close()
+    prep.arenas.close()
+
+
+def encode_frame(prep, timer, frame, tags=None):
+    timed = timer.begin_frame(frame)
+    for k in range(len(prep.kernels)):
+        prep.kernels.encode(k, 0, timer, k if tags is None else tags[k])
+    return timed, timer.resolve()
+
+
+def test_frames_come_back_in_submission_order_with_every_slice(ctx, small):
+    _, _, _, prep = small
+    n = len(prep.kernels)
+    timer = hip.Timer(ctx, n)
+    try:
+        got = []
+        for f in range(3):
+            timed, r = encode_frame(prep, timer, 10 + f, tags=[100 * f + k for k in range(n)])
+            assert timed
+            timer.submitted(r)
+        ctx.synchronize()
+        got = timer.collect()
+        assert [f for f, _ in got] == [10, 11, 12]
+        for i, (_, slices) in enumerate(got):
+            assert [t for t, _ in slices] == [100 * i + k for k in range(n)]
+            assert all(us > 0.0 for _, us in slices)
+        s = timer.stats()
+        assert (s.frames_begun, s.frames_timed, s.frames_skipped, s.frames_failed, s.frames_dropped) == (3, 3, 0, 0, 0)
+    finally:
+        timer.close()
+
+
+def test_a_frame_whose_slot_is_in_flight_is_skipped_not_waited_for(ctx, small):
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, len(prep.kernels))
+    try:
+        for f in range(hip.RING_DEPTH):
+            timed, r = encode_frame(prep, timer, f)
+            assert timed
+            timer.submitted(r)
+        timed, r = encode_frame(prep, timer, hip.RING_DEPTH)
+        assert not timed
+        timer.submitted(r)  # handing back an untimed frame is accepted and ignored
+        ctx.synchronize()
+        assert [f for f, _ in timer.collect()] == list(range(hip.RING_DEPTH))
+        assert timer.stats().frames_skipped == 1
+        timed, r = encode_frame(prep, timer, 99)
+        assert timed
+        timer.submitted(r)
+        ctx.synchronize()
+        assert [f for f, _ in timer.collect()] == [99]
+    finally:
+        timer.close()
+
+
+def test_invalidated_frames_are_never_decoded_and_count_as_failed(ctx, small):
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, len(prep.kernels))
+    try:
+        for f in range(2):
+            _, r = encode_frame(prep, timer, f)
+            timer.submitted(r)
+        assert timer.invalidate_submitted() == 2
+        assert timer.invalidate_submitted() == 0  # already marked
+        ctx.synchronize()
+        assert timer.collect() == []
+        s = timer.stats()
+        assert (s.frames_failed, s.frames_timed) == (2, 0)
+        _, r = encode_frame(prep, timer, 5)
+        timer.submitted(r)
+        ctx.synchronize()
+        assert [f for f, _ in timer.collect()] == [5]
+    finally:
+        timer.close()
+
+
+def test_a_resolved_frame_never_handed_back_is_dropped(ctx, small):
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, len(prep.kernels))
+    try:
+        encode_frame(prep, timer, 0)  # resolved, never submitted
+        _, r = encode_frame(prep, timer, 1)
+        timer.submitted(r)
+        ctx.synchronize()
+        assert [f for f, _ in timer.collect()] == [1]
+        assert timer.stats().frames_dropped == 1
+    finally:
+        timer.close()
+
+
+def test_too_many_slices_in_a_frame_is_an_error(ctx, small):
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, 2)
+    try:
+        timer.begin_frame(0)
+        prep.kernels.encode(0, 0, timer, 0)
+        prep.kernels.encode(1, 0, timer, 1)
+        with pytest.raises(hip.BackendError) as e:
+            prep.kernels.encode(2, 0, timer, 2)
+        assert e.value.code == hip.ERR_TIMER_TOO_MANY_SLICES
+        timer.submitted(timer.resolve())
+        ctx.synchronize()
+        timer.collect()
+    finally:
+        timer.close()
+
+
+def test_the_render_load_spins_for_its_time(ctx):
+    ctx.synchronize()
+    for us in (2000, 8000):
+        t0 = time.perf_counter()
+        ctx.spin(us)
+        ctx.synchronize()
+        took = (time.perf_counter() - t0) * 1e6
+        assert us * 0.98 <= took <= us + 3000, (us, took)
+
+
+def test_the_slice_timer_sees_the_render_load_it_runs_behind(ctx, small):
+    # A slice encoded after the spin starts only when the spin ends, so the
+    # frame's wall time covers both and the slice's own time stays short.
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, 1)
+    try:
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        timer.begin_frame(0)
+        ctx.spin(3000)
+        prep.kernels.encode(0, 0, timer, 7)
+        timer.submitted(timer.resolve())
+        ctx.synchronize()
+        wall = (time.perf_counter() - t0) * 1e6
+        [(frame, [(tag, us)])] = timer.collect()
+        assert (frame, tag) == (0, 7) and 0 < us < 1000 and wall >= 2900
+    finally:
+        timer.close()
+
+
+@pytest.mark.parametrize("bound_us", [frameloop.DEFAULT_MAX_DISPATCH_US, 4])
+def test_the_frame_loop_delivers_every_frame_within_its_latency(ctx, small, bound_us):
+    g, ids, vals, _ = small
+    frames = 24
+    report = frameloop.run(ctx, g, vals, ids.output, hip.F32, frames=frames, period_us=4000, render_us=1500,
+                           bound_us=bound_us, tolerance=1e-4)
+    k = report["latency_frames_k"]
+    assert report["budget_us"] == 2500
+    if report["dropped_periods"] == 0:  # a host that lost whole periods misses their deadlines
+        assert report["missed"] == 0, report
+        assert report["delivered"] == frames - k, report
+    assert report["spent_estimate_us_per_frame_max"] <= report["budget_us"]
+    assert report["output_within_tolerance"], report
+    if bound_us == 4:
+        # Some kernel of this block takes longer than 4 µs: it was split, and
+        # the split program's result still matches the whole one.
+        assert report["kernels_split"] > 0 and report["slices_per_job"] > report["kernels_unsplit"]
+    else:
+        assert report["slices_per_job"] == report["kernels_unsplit"]

@@ -352,3 +352,31 @@ def test_the_high_resolution_loop_spreads_a_block_chain_over_frames():
         delivered += p.delivered
         missed += p.missed
     assert len(delivered) == 6 and not missed
+
+
+def test_the_frame_loop_helpers():
+    from beatlm_amd import frameloop as F
+
+    # The second half of the calibration frames count (calibration.rs:29).
+    assert [f for f in range(F.CALIBRATION_FRAMES + 1) if F.counted(f)][0] == F.CALIBRATION_FRAMES // 2 + 1
+    # The upper middle (stats.rs:145).
+    assert F.median_upper([4, 1, 3, 2]) == 3 and F.median_upper([5]) == 5
+    # The latency a lone job needs is where the scheduler's projection ends,
+    # and a scheduler with that latency delivers it, one frame less misses.
+    for est, budget in (([100] * 24, 1000), ([600] * 24, 8667), ([30, 500, 30, 470], 500)):
+        k = F.latency_for(est, budget, budget)
+        for latency, ok in ((k, True), (k - 1, False)):
+            if latency < 0:
+                continue
+            c = S.CostModel(1, 32, 0.9)
+            for i, e in enumerate(est):
+                c.record(i, e)
+            s = S.Scheduler(latency, S.MISS_DROP, budget)
+            s.submit(frame(0), list(range(len(est))), c)
+            got = []
+            for f in range(latency + 1):
+                p = s.plan_frame(frame(f), budget, c)
+                got += p.delivered
+            assert bool(got) == ok, (est, latency)
+    with pytest.raises(ValueError):
+        F.latency_for([600], 500, 500)
