@@ -188,6 +188,7 @@ _SIGNATURES = {
     "bl_timer_collect": (C.c_int, [_VP, C.POINTER(FrameTiming), C.c_uint32, C.POINTER(C.c_uint32)]),
     "bl_timer_invalidate_submitted": (C.c_int, [_VP]),
     "bl_timer_stats": (C.c_int, [_VP, C.POINTER(TimerStats)]),
+    "bl_kernels_time": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_float)]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
 }
 
@@ -334,6 +335,12 @@ class Kernels:
 
     def encode_all(self, set_index: int = 0) -> None:
         self.ctx.check(self.ctx._lib.bl_kernels_encode_range(self.handle, 0, len(self), set_index))
+
+    def time(self, kernel: int, repeats: int = 20, set_index: int = 0) -> float:
+        """Average µs of one launch over `repeats` back-to-back launches."""
+        us = C.c_float()
+        self.ctx.check(self.ctx._lib.bl_kernels_time(self.handle, kernel, set_index, repeats, C.byref(us)))
+        return float(us.value)
 
     def close(self) -> None:
         if self.handle:

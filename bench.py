@@ -140,25 +140,112 @@ def kernel_bytes(info, elt: int) -> float:
     return 0.0
 
 
-def time_kernels(prep, frames: int, warmup: int = 3):
-    """Median per-kernel µs over `frames` frames, from the slice timer's
-    hipEvent pairs on the backend's stream."""
-    n = len(prep.kernels)
-    timer = hip.Timer(prep.ctx, n)
-    per = [[] for _ in range(n)]
-    for f in range(warmup + frames):
-        timer.begin_frame(f)
-        for k in range(n):
-            prep.kernels.encode(k, 0, timer, k)
-        r = timer.resolve()
-        timer.submitted(r)
-        prep.ctx.synchronize()
-        for frame, slices in timer.collect():
-            if frame >= warmup:
-                for tag, us in slices:
-                    per[tag].append(us)
-    timer.close()
-    return [statistics.median(p) if p else float("nan") for p in per]
+def bracketed(ctx, prep, ks, repeats):
+    """Per-launch µs of each kernel in `ks` (alone, back to back), between two
+    zero-length spin launches that mark the span in a counter profile."""
+    ctx.synchronize()
+    ctx.spin(0)
+    us = [prep.kernels.time(k, repeats) for k in ks]
+    ctx.spin(0)
+    ctx.synchronize()
+    return us
+
+
+TRAFFIC_DIR = os.path.join(ROOT, "profiles")
+
+
+def traffic_file(config: str, math_name: str) -> str:
+    return os.path.join(TRAFFIC_DIR, f"hbm_traffic_{config}_{math_name}.txt")
+
+
+def read_traffic(config: str, math_name: str) -> dict:
+    """Bytes per launch measured by the counter profile of this workload:
+    {(tag, group): bytes}, from its `traffic` lines; empty when there is none."""
+    out = {}
+    try:
+        with open(traffic_file(config, math_name)) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 4 and parts[0] == "traffic":
+                    out[(parts[1], parts[2])] = float(parts[3])
+    except FileNotFoundError:
+        pass
+    return out
+
+
+def pmc_summary(directory: str) -> str:
+    """The counter summary of a profile directory holding four rocprofv3 --pmc
+    runs (pmc_FETCH_SIZE, pmc_WRITE_SIZE of this bench; copy_FETCH_SIZE,
+    copy_WRITE_SIZE of a 256 MiB device copy) and the bench's JSON line in
+    pmc_FETCH_SIZE.log. Each counter is scaled by what it reads for the copy
+    (bytes moved / counter KiB). The dispatches between the bench's marker
+    launches (spin_kernel) are the bracketed group's: (repeats + 1) launches of
+    each of its kernels."""
+    import csv
+
+    def rows(name):
+        with open(os.path.join(directory, name, "run_counter_collection.csv")) as f:
+            return sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
+
+    copy_bytes = 256 << 20
+    scale = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        vals = [float(r["Counter_Value"]) for r in rows(f"copy_{c}") if "copyBuffer" in r["Kernel_Name"]]
+        vals.sort()
+        scale[c] = copy_bytes / (vals[len(vals) // 2] * 1024.0)
+    with open(os.path.join(directory, "pmc_FETCH_SIZE.log")) as f:
+        line = next(l for l in f if l.startswith("{") and '"metric"' in l)
+    bench = json.loads(line)
+    out = [f"# counter scale from a {copy_bytes >> 20} MiB copy: FETCH_SIZE x{scale['FETCH_SIZE']:.4f}, "
+           f"WRITE_SIZE x{scale['WRITE_SIZE']:.4f} (bytes per counter KiB / 1024)"]
+    per = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        rs = rows(f"pmc_{c}")
+        marks = [i for i, r in enumerate(rs) if "spin_kernel" in r["Kernel_Name"]]
+        spans = [rs[marks[2 * j] + 1: marks[2 * j + 1]] for j in range(len(marks) // 2)]
+        for b, span in zip(bench["brackets"], spans):
+            kib = sum(float(r["Counter_Value"]) for r in span)
+            per.setdefault((b["tag"], b["group"]), {})[c] = (kib, len(span), b)
+            by_kernel = {}
+            for r in span:
+                name = r["Kernel_Name"].split("(bl::")[0].replace("void bl::(anonymous namespace)::", "")
+                by_kernel.setdefault(name, []).append(float(r["Counter_Value"]))
+            for name, v in by_kernel.items():
+                out.append(f"# {b['tag']:10s} {c:10s} {name:48s} dispatches {len(v):4d}  "
+                           f"mean {sum(v) / len(v):12.1f} KiB")
+    for (tag, group), cs in per.items():
+        b = cs["FETCH_SIZE"][2]
+        launches = (b["repeats"] + 1) * b["kernels"]
+        fetch = cs["FETCH_SIZE"][0] * 1024 * scale["FETCH_SIZE"] / launches
+        write = cs["WRITE_SIZE"][0] * 1024 * scale["WRITE_SIZE"] / launches
+        out.append(f"# {tag} {group}: per launch {fetch / 1e6:.3f} MB fetched + {write / 1e6:.3f} MB written")
+        out.append(f"traffic {tag} {group} {fetch + write:.0f}")
+    return "\n".join(out) + "\n"
+
+
+def layernorm_hbm(ctx, rows: int, width: int, repeats: int = 20) -> dict:
+    """One LayerNorm of `rows` x `width` f32 rows, larger than the caches, timed
+    alone: algorithmic bytes (read x, write y, read gamma and beta) over the
+    median launch time, against the HBM peak."""
+    g = ir.Graph()
+    g.tensor(1, ir.WEIGHT, rows * width)
+    g.tensor(2, ir.WEIGHT, width)
+    g.tensor(3, ir.WEIGHT, width)
+    g.tensor(4, ir.OUTPUT, rows * width)
+    g.push(ir.op(ir.OP_LAYER_NORM, [1, 2, 3], [rows, width], EPS), 4)
+    prep = ir.prepare(ctx, g, flash=False)
+    rng = np.random.default_rng(11)
+    prep.write(1, rng.standard_normal(rows * width, dtype=np.float32))
+    prep.write(2, 1 + 0.1 * rng.standard_normal(width, dtype=np.float32))
+    prep.write(3, 0.1 * rng.standard_normal(width, dtype=np.float32))
+    us = bracketed(ctx, prep, [0], repeats)[0]
+    prep.kernels.close()
+    prep.arenas.close()
+    nbytes = 4.0 * (2 * rows * width + 2 * width)
+    gbs = nbytes / us / 1e3
+    return {"rows": rows, "width": width, "dtype": "f32", "algorithmic_bytes_per_launch": int(nbytes),
+            "us_per_launch": round(us, 2), "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
 def cpu_baseline(cfg, tokens, threads):
@@ -198,11 +285,16 @@ def main() -> int:
     ap.add_argument("--config", default="vit-s-518", choices=sorted(CONFIGS))
     ap.add_argument("--f32-math", default="split", choices=["split", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-frames", type=int, default=20)
+    ap.add_argument("--kernel-repeats", type=int, default=20)
+    ap.add_argument("--pmc-summary", metavar="DIR", help="write the counter summary of a profile directory and exit")
     ap.add_argument("--frame-loop-frames", type=int, default=120)
+    ap.add_argument("--layernorm-rows", type=int, default=262144)
     ap.add_argument("--render-us", type=int, default=8000)
     ap.add_argument("--max-dispatch-us", type=int, default=frameloop.DEFAULT_MAX_DISPATCH_US)
     args = ap.parse_args()
+    if args.pmc_summary:
+        sys.stdout.write(pmc_summary(args.pmc_summary))
+        return 0
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -248,39 +340,50 @@ def main() -> int:
     blocks_per_step = cfg["blocks"] * frames
     us_per_block = ms_per_step * 1e3 / blocks_per_step
 
-    # Per-kernel times from hipEvent pairs, for the roofline.
-    med = time_kernels(prep, args.profile_frames)
-    infos = [prep.program.kernel(k) for k in range(len(prep.program))]
-    labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
-    by_kind: dict[str, list[float]] = {}
-    flops_kind: dict[str, float] = {}
-    bytes_kind: dict[str, float] = {}
-    for k, info in enumerate(infos):
-        name = prep.program.name(k)
-        by_kind.setdefault(name, []).append(med[k])
-        flops_kind[name] = kernel_flops(info)
-        bytes_kind[name] = kernel_bytes(info, elt)
-    totals = {n: sum(v) for n, v in by_kind.items()}
+    # Per-launch durations: each kernel alone, back to back, between a hipEvent
+    # pair on the backend's stream (what a kernel trace reports per dispatch).
+    n_kernels = len(prep.kernels)
+    per_launch = [prep.kernels.time(k, args.kernel_repeats) for k in range(n_kernels)]
+    infos = [prep.program.kernel(k) for k in range(n_kernels)]
+    groups: dict[str, list[int]] = {}
+    for k in range(n_kernels):
+        groups.setdefault(prep.program.name(k), []).append(k)
+    totals = {g: sum(per_launch[k] for k in ks) for g, ks in groups.items()}
     dominant = max(totals, key=totals.get)
-    avg_us = statistics.mean(by_kind[dominant])
 
     math_name = "f16" if dtype == hip.F16 else ("bf16x3" if args.f32_math == "split" else "f32")
     # An f32 product on bf16 matrix cores is three bf16 MFMAs.
     mfma_peak = PEAK_TFLOPS["f16"] if dtype == hip.F16 else (
         PEAK_TFLOPS["bf16"] / 3.0 if args.f32_math == "split" else PEAK_TFLOPS["f32"]
     )
+    traffic = read_traffic(args.config, math_name)
+    brackets = []
 
-    def roof(name):
-        us = statistics.mean(by_kind[name])
-        if flops_kind[name] > 0:
-            a = flops_kind[name] / us / 1e6
+    def roof(group, tag):
+        """The group's launches re-timed between two zero-length spin launches,
+        which mark the span in a counter profile; achieved = algorithmic work of
+        one launch of each kernel over their summed per-launch time."""
+        ks = groups[group]
+        us = bracketed(ctx, prep, ks, args.kernel_repeats)
+        brackets.append({"tag": tag, "group": group, "kernels": len(ks), "repeats": args.kernel_repeats})
+        t = sum(us)
+        flops = sum(kernel_flops(infos[k]) for k in ks)
+        nbytes = sum(kernel_bytes(infos[k], elt) for k in ks)
+        hbm = traffic.get((tag, group))
+        common = {"kernel": group, "launches": len(ks), "us_per_launch": round(t / len(ks), 2),
+                  "algorithmic_bytes_per_launch": int(nbytes / len(ks)),
+                  "traffic": int(hbm) if hbm is not None else None}
+        if flops > 0:
+            a = flops / t / 1e6
             return {"bound": "mfma", "achieved": round(a, 2), "peak": round(mfma_peak, 1), "unit": "TFLOP/s",
-                    "frac": round(a / mfma_peak, 4), "traffic": None, "kernel": name, "us_per_launch": round(us, 2)}
-        a = bytes_kind[name] / us / 1e3
+                    "frac": round(a / mfma_peak, 4), **common,
+                    "algorithmic_flop_per_launch": int(flops / len(ks))}
+        a = nbytes / t / 1e3
         return {"bound": "hbm", "achieved": round(a, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(a / PEAK_HBM_GBS, 4), "traffic": None, "kernel": name, "us_per_launch": round(us, 2)}
+                "frac": round(a / PEAK_HBM_GBS, 4), **common}
 
-    attn = roof("flash_attention") if "flash_attention" in by_kind else None
+    roofline = roof(dominant, "roofline")
+    attn = roof("flash_attention", "attention") if "flash_attention" in groups else None
     result = {
         "metric": METRIC,
         "value": round(us_per_block, 2),
@@ -304,14 +407,22 @@ def main() -> int:
             "matrix_math": math_name,
             "kernels_per_frame": len(prep.kernels),
         },
-        "roofline": roof(dominant),
+        "roofline": roofline,
         "attention": attn,
-        "per_kernel_us": {n: round(statistics.mean(v), 2) for n, v in by_kind.items()},
-        "kernel_sum_us_per_block": round(sum(med) / cfg["blocks"], 2),
+        "per_kernel_us": {g: round(statistics.mean(per_launch[k] for k in ks), 2) for g, ks in groups.items()},
+        "kernel_sum_us_per_block": round(sum(per_launch) / cfg["blocks"], 2),
     }
     if attn:
         result["attention_tflops"] = attn["achieved"]
         result["attention_frac_of_mfma_peak"] = attn["frac"]
+
+    if args.layernorm_rows > 0:
+        ln = layernorm_hbm(ctx, args.layernorm_rows, 384, args.kernel_repeats)
+        group = f"layernorm_{args.layernorm_rows}x384"
+        brackets.append({"tag": "layernorm", "group": group, "kernels": 1, "repeats": args.kernel_repeats})
+        hbm = traffic.get(("layernorm", group))
+        ln["traffic"] = int(hbm) if hbm is not None else None
+        result["layernorm_hbm"] = ln
 
     if args.frame_loop_frames > 0:
         hi = CONFIGS["vit-s-1036"]
@@ -334,6 +445,7 @@ def main() -> int:
             "sample": f"one f32 block ({tokens} tokens) of the reference's WGSL kernels restated in C "
             "(oracle, same summation order), OpenMP over rows; 1 warm-up, median of 5",
         }
+    result["brackets"] = brackets
     print(json.dumps(result))
     return 0
 

@@ -239,6 +239,13 @@ int bl_kernels_encode(bl_kernels *kernels, uint32_t kernel, uint32_t set,
 int bl_kernels_encode_range(bl_kernels *kernels, uint32_t first, uint32_t count,
                             uint32_t set);
 
+/* The average duration of one launch of `kernel`, from a hipEvent pair on the
+ * context's stream around `repeats` back-to-back launches (after one untimed
+ * launch). Blocks until they finish. No counterpart in the reference, which
+ * times kernels only through the slice timer: a measurement aid for per-kernel
+ * rooflines, free of the launch gaps a per-slice event pair includes. */
+int bl_kernels_time(bl_kernels *kernels, uint32_t kernel, uint32_t set, uint32_t repeats, float *micros_per_launch);
+
 /* ---- slice timer: hipEvent pairs per slice, a ring of frames ---- */
 #define BL_TIMER_RING_DEPTH 3
 typedef struct {
