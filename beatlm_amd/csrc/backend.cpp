@@ -30,6 +30,10 @@ struct bl_ctx {
     uint32_t compute_units = 0;
     uint32_t wall_clock_khz = 0;
     bl_device_profile_t profile{};
+    // Arenas, kernels and timers made from this context and not yet destroyed;
+    // bl_ctx_destroy waits for the last of them before releasing the stream.
+    uint32_t children = 0;
+    bool closed = false;
 };
 
 namespace {
@@ -118,14 +122,25 @@ extern "C" int bl_ctx_create(int device_ordinal, bl_ctx **out) {
     return BL_OK;
 }
 
-extern "C" void bl_ctx_destroy(bl_ctx *ctx) {
-    if (!ctx) return;
+static void ctx_free(bl_ctx *ctx) {
     hipSetDevice(ctx->device);
     if (ctx->stream) {
         hipStreamSynchronize(ctx->stream);
         hipStreamDestroy(ctx->stream);
     }
     delete ctx;
+}
+
+extern "C" void bl_ctx_destroy(bl_ctx *ctx) {
+    if (!ctx || ctx->closed) return;
+    ctx->closed = true;
+    if (ctx->children == 0) ctx_free(ctx);
+}
+
+void bl_ctx_retain(bl_ctx *ctx) { ctx->children++; }
+
+void bl_ctx_release(bl_ctx *ctx) {
+    if (--ctx->children == 0 && ctx->closed) ctx_free(ctx);
 }
 
 extern "C" const char *bl_last_error(const bl_ctx *ctx) { return ctx ? ctx->error.c_str() : "no context"; }
@@ -204,6 +219,7 @@ extern "C" int bl_arenas_create(bl_ctx *ctx, const uint64_t *sizes, uint32_t n, 
         ctx->allocations++;
         a->base = (char *)p;
     }
+    bl_ctx_retain(ctx);
     *out = a;
     return BL_OK;
 }
@@ -215,7 +231,9 @@ extern "C" void bl_arenas_destroy(bl_arenas *a) {
         hipStreamSynchronize(a->ctx->stream);
         hipFree(a->base);
     }
+    bl_ctx *ctx = a->ctx;
     delete a;
+    bl_ctx_release(ctx);
 }
 
 static int check_range(bl_arenas *a, uint32_t arena, uint64_t offset, uint64_t bytes) {
@@ -695,20 +713,27 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
             case BL_MAIN_FLASH_ATTENTION: {
                 if (s.n_epilogue) return bad(BL_ERR_KERNEL, "kernel %s: the flash kernel takes no epilogue", name.c_str());
                 L.family = Family::FLASH;
-                const uint32_t rows = pt.end - pt.start;
-                const uint32_t wgs = (rows + FLASH_ROWS - 1) / FLASH_ROWS * d[1];
                 const uint32_t t_pad = (d[0] + 63) / 64 * 64;
-                const uint32_t ntiles = t_pad / 64;
-                // Enough workgroups for two per CU, each split keeping two key tiles or more.
-                uint32_t splits = (2 * ctx->compute_units + wgs - 1) / wgs;
-                splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, ntiles / 2, FLASH_MAX_SPLITS}));
-                L.fl = FlashArgs{rd(0), out_ptr, nullptr, nullptr, nullptr, nullptr, d[0], d[1], t_pad, pt.start, pt.end, splits, s.scale};
-                uint64_t need_bytes = flash_operand_bytes(fmath, d[1], t_pad);
-                if (splits > 1) need_bytes += (uint64_t)splits * d[0] * d[1] * (FLASH_HEAD_DIM + 2) * sizeof(float);
-                scratch_bytes = std::max(scratch_bytes, need_bytes);
+                const FlashPlan fp = plan_flash(fmath, d[0], d[1], pt.start, pt.end, ctx->compute_units);
+                L.fl = FlashArgs{};
+                L.fl.qkv = rd(0);
+                L.fl.out = out_ptr;
+                L.fl.tokens = d[0];
+                L.fl.heads = d[1];
+                L.fl.t_pad = t_pad;
+                L.fl.row0 = pt.start;
+                L.fl.row1 = pt.end;
+                L.fl.splits = fp.splits;
+                L.fl.scale = s.scale;
+                L.fl.qtiles = fp.qtiles;
+                L.fl.wgs = fp.wgs;
+                L.fl.units = fp.units;
+                L.fl.merge = fp.merge;
+                scratch_bytes = std::max(scratch_bytes, fp.scratch_bytes);
                 flash_users.push_back({ki, si});
-                variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
-                          " splits=" + std::to_string(splits);
+                variant = fmath == Math::F32 ? "mfma-f32 splits=" + std::to_string(fp.splits)
+                                             : std::string(fmath == Math::F16 ? "mfma-f16" : "mfma-bf16x3") + " 32x32 runs=" +
+                                                   std::to_string(fp.wgs) + (fp.merge ? " merged" : "");
                 break;
             }
             }
@@ -740,17 +765,10 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
         if (!ks->scratch) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
         // Kernels run one after another on the stream, so every flash kernel
         // uses the same scratch: operands, then partial outputs and statistics.
-        for (auto [ki, si] : flash_users) {
-            FlashArgs &f = ks->kernels[ki].per_set[si].fl;
-            const Math fm = ks->kernels[ki].per_set[si].math;
-            const uint64_t operands = flash_operand_bytes(fm, f.heads, f.t_pad);
-            char *base = (char *)ks->scratch;
-            f.kp = base;
-            f.vt = base + operands / 2;
-            f.partial = (float *)(base + operands);
-            f.stats = f.partial + (uint64_t)f.splits * f.tokens * f.heads * FLASH_HEAD_DIM;
-        }
+        for (auto [ki, si] : flash_users)
+            bind_flash_scratch(ks->kernels[ki].per_set[si].fl, ks->kernels[ki].per_set[si].math, ks->scratch);
     }
+    bl_ctx_retain(ctx);
     *out = ks;
     return BL_OK;
 }
@@ -761,7 +779,9 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
     hipStreamSynchronize(k->ctx->stream);
     if (k->scratch) hipFree(k->scratch);
     if (k->pack_buffer) hipFree(k->pack_buffer);
+    bl_ctx *ctx = k->ctx;
     delete k;
+    bl_ctx_release(ctx);
 }
 
 extern "C" uint32_t bl_kernels_len(const bl_kernels *k) { return k ? (uint32_t)k->kernels.size() : 0; }

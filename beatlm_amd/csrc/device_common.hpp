@@ -10,6 +10,7 @@
 
 namespace bl {
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -40,6 +41,18 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
     return v;
+}
+
+// ---- lane l and lane l ^ 32 (v_permlane32_swap: no LDS round trip) ----
+// The swap exchanges lanes 32-63 of its first operand with lanes 0-31 of its
+// second; with v in both, the two results hold (v[l], v[l ^ 32]) in some order.
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // ---- GELU through erf ----
@@ -125,18 +138,16 @@ __device__ __forceinline__ int swz(int row, int chunk) {
     else return chunk ^ (row & 15);
 }
 
-// Issues one operand's direct loads for one stage: `rows` rows of CPR chunks,
-// the chunks spread over the 4 waves in lane order.
 // One operand's direct loads for one stage: ROWS rows of CPR 16-byte chunks,
-// spread over the 4 waves in lane order. The lane's byte offsets from the
+// spread over the NWAVES waves of the workgroup in lane order. The lane's byte offsets from the
 // operand's tile base (its row, clamped to `row_limit`, and its swizzled
 // chunk) are computed once; a stage then costs one address add per load.
-template <int ROWS, int CPR>
+template <int ROWS, int CPR, int NWAVES = 4>
 struct RowLoader {
     static constexpr int TOTAL = ROWS * CPR;
-    static constexpr int PER_WAVE = TOTAL / 4;
+    static constexpr int PER_WAVE = TOTAL / NWAVES;
     static constexpr int INSTR = (PER_WAVE + 63) / 64;
-    static_assert(TOTAL % 4 == 0, "chunks per wave");
+    static_assert(TOTAL % NWAVES == 0, "chunks per wave");
     uint32_t off[INSTR];
     bool active[INSTR];
     int wave;
@@ -163,7 +174,7 @@ struct RowLoader {
     }
 };
 
-template <int ROWS, int CPR>
-constexpr int loads_per_wave() { return ((ROWS * CPR / 4) + 63) / 64; }
+template <int ROWS, int CPR, int NWAVES = 4>
+constexpr int loads_per_wave() { return ((ROWS * CPR / NWAVES) + 63) / 64; }
 
 }  // namespace bl

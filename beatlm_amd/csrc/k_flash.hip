@@ -1,30 +1,42 @@
 // Fused multi-head self-attention for one qkv tensor: the reference's three
 // kernels attention_scores+scale -> softmax -> attention_values
 // (crates/beatlm-core/src/kernel.rs:731-777; codegen/wgsl.rs:590-669,
-// :975-1010) as one flash-style kernel with an online softmax, so the
+// :975-1010) as one flash-style pass with an online softmax, so the
 // [T][H][T] scores and probabilities never exist.
 //
 //   qkv  [T][3][H][64]  (queries, keys, values of each token, heads side by side)
 //   out  [T][H * 64]    (heads side by side, as the output projection reads them)
 //
-// Three launches per spec:
+// Launches per spec:
 //  1. flash_prep_kernel writes the keys as K [H][T_pad][64] and the values
 //     transposed as Vt [H][64][T_pad], once, in the matrix cores' operand type
-//     (f16, f32, or hi and lo bf16 planes), zero-padded to whole 64-key tiles;
-//  2. flash_kernel: a workgroup of 4 waves owns 64 query rows of one head and
-//     one range of key tiles; K and Vt tiles stream through a ring of LDS
-//     stages filled by direct 16-byte loads. Each wave computes the transposed
-//     scores S^T = K Q^T for its 16 queries, so a lane's accumulators hold 16
-//     keys of ONE query (query = lane % 16): the online softmax's row max and
-//     row sum are per-lane values plus two cross-lane steps, and the
-//     probabilities are already laid out as the B operand of O^T = V^T P^T,
-//     whose accumulators hold the same query per lane, so the rescale by
-//     exp(m_old - m_new) is one multiply per register. Softmax in base 2:
-//     s * scale * log2(e) and exp2;
-//  3. when the key range was split across workgroups (too few query tiles to
-//     fill 256 CUs), flash_merge_kernel combines the splits' (max, sum,
-//     unnormalised output).
+//     (f16, f32, or hi and lo bf16 planes), zero-padded to whole 64-key tiles.
+//     For the 32 x 32 kernel each 16-key group of a Vt row is stored in the
+//     order 0-3, 8-11, 4-7, 12-15 (bits 2 and 3 of the key swapped), which is
+//     the order in which that kernel's probabilities come out of its score
+//     accumulators.
+//  2. attn_kernel (f16 and bf16x3 math): the (head, 4 x QB x 32 query rows,
+//     64-key tile) units are dealt out in equal contiguous runs to a fixed
+//     grid of workgroups (two per CU), so every CU gets the same amount of
+//     work whatever T and H are. A workgroup walks its run as segments of one
+//     (head, query tile) each; its 4 waves own QB blocks of 32 queries and
+//     share the K and Vt tiles, which stream through an LDS ring filled by
+//     direct 16-byte loads. Each wave computes the transposed scores
+//     S^T = K Q^T with v_mfma_f32_32x32x16, so a lane's accumulators hold 16
+//     keys of ONE query: the row max is lane-local plus one exchange with the
+//     lane 32 away. Eight consecutive accumulators are then exactly the
+//     B operand of O^T = V^T P^T for one 16-key step. The running max is only
+//     raised when a tile's max exceeds it by more than 8 (in log2 units), so
+//     most tiles skip the rescale of O; probabilities stay <= 2^8.
+//     A segment that covers all keys of its query tile writes the output; one
+//     that covers part of them writes (max, sum, unnormalised output) to
+//     scratch, and flash_merge_kernel combines them.
+//  3. flash16_kernel (f32 math, v_mfma_f32_16x16x4_f32): a workgroup owns 64
+//     queries of one head and one range of key tiles (split when there are
+//     too few query tiles to fill the chip); merged by flash16_merge_kernel.
 // Query rows outside the part are not stored.
+#include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "device_common.hpp"
@@ -36,35 +48,45 @@ constexpr int THREADS = 256;
 constexpr int KT = 64;  // keys per tile
 constexpr int HD = 64;  // head width
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr int NW = 8;   // waves per workgroup of the 32 x 32 kernel (two per SIMD)
+constexpr int THREADS32 = NW * 64;
+// A tile's max must exceed the running max by more than this (log2 units)
+// before the running max moves: probabilities are then at most 2^RESCALE.
+constexpr float RESCALE = 8.0f;
 
 template <Math M> struct FlashTraits;
 template <> struct FlashTraits<Math::F16> {
     using T = _Float16;   // storage of qkv and out
     using L = _Float16;   // operand element of K / Vt
-    static constexpr int PLANES = 1;
-    static constexpr int CPR = 8;     // 16-byte chunks per 64-element row
-    static constexpr int STAGES = 3;
+    static constexpr int PLANES = 1;  // operand planes (hi and lo for bf16x3)
+    static constexpr int STAGES = 4;  // LDS ring depth
+    static constexpr int QB = 1;      // 32-query blocks per wave
 };
 template <> struct FlashTraits<Math::SPLIT> {
     using T = float;
     using L = __bf16;
     static constexpr int PLANES = 2;
-    static constexpr int CPR = 8;
-    static constexpr int STAGES = 2;
+    static constexpr int STAGES = 4;
+    static constexpr int QB = 1;
 };
 template <> struct FlashTraits<Math::F32> {
     using T = float;
     using L = float;
-    static constexpr int PLANES = 1;
-    static constexpr int CPR = 16;
+    static constexpr int CPR = 16;    // 16-byte chunks per 64-element row
     static constexpr int STAGES = 2;
 };
+
+// Query rows of one unit (a workgroup's tile) of the 32 x 32 kernel.
+template <Math M> constexpr uint32_t query_rows() { return NW * FlashTraits<M>::QB * 32; }
+
+// Position of key k inside its Vt row for the 32 x 32 kernel: bits 2 and 3 swapped.
+__host__ __device__ constexpr uint32_t vt_pos(uint32_t k) { return (k & ~12u) | ((k & 4u) << 1) | ((k & 8u) >> 1); }
 
 // ---- 1. K and Vt in operand layout ----
 // One workgroup per 64 keys of one head: 16-byte loads of the key and value
 // rows, keys written as they are, values transposed through LDS and written
-// as rows of 64 keys.
-template <Math M>
+// as rows of 64 keys (in vt_pos order when PERM).
+template <Math M, bool PERM>
 __global__ __launch_bounds__(THREADS) void flash_prep_kernel(FlashArgs a) {
     using Tr = FlashTraits<M>;
     using T = typename Tr::T;
@@ -109,7 +131,7 @@ __global__ __launch_bounds__(THREADS) void flash_prep_kernel(FlashArgs a) {
     __syncthreads();
     for (int c = threadIdx.x; c < HD * KT / 4; c += THREADS) {
         const int d = c / (KT / 4), r = (c % (KT / 4)) * 4;
-        const uint64_t vi = ((uint64_t)head * HD + d) * tpad + kbase + r;
+        const uint64_t vi = ((uint64_t)head * HD + d) * tpad + kbase + (PERM ? vt_pos(r) : r);
         if constexpr (M == Math::SPLIT) {
             bf16x4 h, l;
 #pragma unroll
@@ -132,21 +154,440 @@ __global__ __launch_bounds__(THREADS) void flash_prep_kernel(FlashArgs a) {
     }
 }
 
-// ---- 2. the attention ----
+// ---- 2. the 32 x 32 kernel (f16, bf16x3) ----
+
+template <Math M> struct Op32;
+template <> struct Op32<Math::F16> {
+    using V = f16x8;
+    static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Op32<Math::SPLIT> {
+    using V = bf16x8;
+    static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+// The bias product that starts each score chain. Key side (A, lane l32 =
+// key, slots of lanes 0-31 only): [1, mask], mask = BIG for a key past the
+// last token. Query side (B): [-m, -1]. The result is -m, or -m - BIG.
+template <Math M> struct BiasBig;
+template <> struct BiasBig<Math::F16> { static constexpr float value = 60000.0f; };
+template <> struct BiasBig<Math::SPLIT> { static constexpr float value = 1e30f; };
+
 template <Math M>
-__global__ __launch_bounds__(THREADS) void flash_kernel(FlashArgs args) {
+__device__ __forceinline__ typename Op32<M>::V bias_a(bool low_lanes, bool masked) {
+    using V8 = typename Op32<M>::V;
+    using E = std::remove_cv_t<std::remove_reference_t<decltype(V8{}[0])>>;
+    V8 a = {};
+    a[0] = (E)(low_lanes ? 1.0f : 0.0f);
+    a[1] = (E)(low_lanes && masked ? BiasBig<M>::value : 0.0f);
+    return a;
+}
+template <Math M>
+__device__ __forceinline__ typename Op32<M>::V bias_b(float m, int h) {
+    using V8 = typename Op32<M>::V;
+    using E = std::remove_cv_t<std::remove_reference_t<decltype(V8{}[0])>>;
+    V8 b = {};
+    b[0] = (E)(h == 0 ? -m : 0.0f);
+    b[1] = (E)(h == 0 ? -1.0f : 0.0f);
+    return b;
+}
+// The nearest value of the operand type (kept within f16's range), so the
+// bias product subtracts exactly the offset o and l carry.
+template <Math M> __device__ __forceinline__ float representable(float v);
+template <> __device__ __forceinline__ float representable<Math::F16>(float v) {
+    return (float)(_Float16)fminf(fmaxf(v, -30000.0f), 30000.0f);
+}
+template <> __device__ __forceinline__ float representable<Math::SPLIT>(float v) { return (float)(__bf16)v; }
+
+// The run of units [begin, end) of virtual workgroup v out of G: equal
+// contiguous shares of U. The planner keeps U * G below 2^32.
+__host__ __device__ inline uint32_t run_begin(uint32_t v, uint32_t U, uint32_t G) { return v * U / G; }
+// The virtual workgroup whose run holds unit u.
+__host__ __device__ inline uint32_t run_of(uint32_t u, uint32_t U, uint32_t G) { return ((u + 1) * G - 1) / U; }
+
+template <Math M>
+__global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
     using Tr = FlashTraits<M>;
     using T = typename Tr::T;
-    using L = typename Tr::L;
-    constexpr int CPR = Tr::CPR, PLANES = Tr::PLANES, STAGES = Tr::STAGES;
-    constexpr int TILE_BYTES = 64 * CPR * 16;  // one plane of a K or Vt tile
+    using Op = Op32<M>;
+    using V8 = typename Op::V;
+    constexpr int PLANES = Tr::PLANES, STAGES = Tr::STAGES;
+    constexpr int CPR = 8;
+    constexpr int ROWB = CPR * 16;             // 128 bytes per staged row
+    constexpr int TILE_BYTES = 64 * ROWB;      // one plane of a K or Vt tile
     constexpr int K_BYTES = PLANES * TILE_BYTES;
     constexpr int STAGE_BYTES = 2 * K_BYTES;
-    constexpr int LPS = 2 * PLANES * loads_per_wave<64, CPR>();
+    constexpr int LPS = 2 * PLANES * loads_per_wave<64, CPR, NW>();
+    constexpr uint32_t QROWS = query_rows<M>();
+    constexpr bool SPLIT = M == Math::SPLIT;
+    static_assert(Tr::QB == 1, "one 32-query block per wave");
+    static_assert(STAGES >= 3, "two tiles are read while the next is loaded");
 
     __shared__ __attribute__((aligned(16))) char smem[STAGES * STAGE_BYTES];
 
-    const T *__restrict__ qkv = (const T *)args.qkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const uint32_t H = args.heads, tpad = args.t_pad, Tn = args.tokens;
+    const uint32_t kt = tpad / KT;
+    const uint32_t U = args.units;
+    const uint32_t G = args.wgs, g = blockIdx.x;
+    // Consecutive workgroups go to different XCDs (round robin over 8); give
+    // the workgroups of one XCD consecutive runs, so they share heads and key
+    // ranges in that XCD's L2.
+    const uint32_t v = (G % 8 == 0) ? (g % 8) * (G / 8) + g / 8 : g;
+    const uint32_t u_begin = run_begin(v, U, G), u_end = run_begin(v + 1, U, G);
+
+    constexpr int ESZ = 2;
+    const uint64_t plane_bytes = (uint64_t)H * tpad * HD * ESZ;
+    const RowLoader<64, CPR, NW> kload(HD * ESZ, 63, wave, lane);
+    const RowLoader<64, CPR, NW> vload(tpad * ESZ, 63, wave, lane);
+    const float c = args.scale * LOG2E;
+    const uint32_t row_stride = 3 * H * HD;
+    // Fragment reads: staged row 32 b + l32 carries the swizzle of l32.
+    const int x = (l32 >> 1) & 7;
+    const int lrow = l32 * ROWB;
+
+    uint32_t u = u_begin;
+    bool first = true;
+    while (u < u_end) {
+        const uint32_t item = u / kt;
+        const uint32_t k0 = u % kt;
+        const uint32_t left = u_end - u;
+        const uint32_t k1 = left < kt - k0 ? k0 + left : kt;
+        const uint32_t head = item / args.qtiles, qt = item % args.qtiles;
+        const uint32_t q = args.row0 + qt * QROWS + wave * 32 + l32;
+
+        const char *kbase = (const char *)args.kp + (uint64_t)head * tpad * HD * ESZ;
+        const char *vbase = (const char *)args.vt + (uint64_t)head * HD * tpad * ESZ;
+        auto issue = [&](uint32_t t) {
+            char *st = smem + ((t - k0) % STAGES) * STAGE_BYTES;
+#pragma unroll
+            for (int p = 0; p < PLANES; p++) {
+                kload.issue(kbase + p * plane_bytes + (uint64_t)t * KT * HD * ESZ, st + p * TILE_BYTES);
+                vload.issue(vbase + p * plane_bytes + (uint64_t)t * KT * ESZ, st + K_BYTES + p * TILE_BYTES);
+            }
+        };
+        // Tile t has landed for every wave once this wave's loads up to it are
+        // done (at most the later tiles' loads outstanding) and all waves met.
+        auto arrive = [&](uint32_t t) {
+            if (t + STAGES - 3 <= k1 - 1) wait_vmcnt<(STAGES - 3) * LPS>();
+            else wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        };
+
+        // The wave's 32 queries, pre-scaled by scale * log2(e), as the B operand
+        // of S^T = K Q^T: lane (l32, h) holds d = 16 ds + 8 h + e of query q.
+        V8 qh[4], ql[4];
+        {
+            const bool ok = q < args.row1;
+            const T *qrow = (const T *)args.qkv + (uint64_t)q * row_stride + head * HD + 8 * h;
+#pragma unroll
+            for (int ds = 0; ds < 4; ds++) {
+                if constexpr (SPLIT) {
+                    f32x4 a = {}, b = {};
+                    if (ok) {
+                        a = *(const f32x4 *)(qrow + 16 * ds);
+                        b = *(const f32x4 *)(qrow + 16 * ds + 4);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        __bf16 hi, lo;
+                        split_bf16((e < 4 ? a[e] : b[e - 4]) * c, hi, lo);
+                        qh[ds][e] = hi;
+                        ql[ds][e] = lo;
+                    }
+                } else {
+                    f16x8 a = {};
+                    if (ok) a = *(const f16x8 *)(qrow + 16 * ds);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) qh[ds][e] = (_Float16)((float)a[e] * c);
+                }
+            }
+        }
+
+        // S^T - bias for tile t: keys 32 mb + 8 (i/4) + 4 h + i%4, query q. Each
+        // chain starts with the bias product: key slots [1, mask] (mask = BIG
+        // for a key past the last token) times query slots [-bias, -1] in the
+        // k-slots of lanes 0-31.
+        auto scores = [&](uint32_t t, const V8 &bq, f32x16 (&s)[2]) {
+            const char *ks = smem + ((t - k0) % STAGES) * STAGE_BYTES + lrow;
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++) {
+                const uint32_t key = t * KT + 32 * mb + l32;
+                s[mb] = Op::mma(bias_a<M>(h == 0, key >= Tn), bq, f32x16{});
+#pragma unroll
+                for (int ds = 0; ds < 4; ds++) {
+                    const int off = mb * 32 * ROWB + (((2 * ds + h) ^ x) << 4);
+                    const V8 kh = *(const V8 *)(ks + off);
+                    if constexpr (SPLIT) {
+                        const V8 kl = *(const V8 *)(ks + TILE_BYTES + off);
+                        s[mb] = Op::mma(kl, qh[ds], s[mb]);
+                        s[mb] = Op::mma(kh, ql[ds], s[mb]);
+                        s[mb] = Op::mma(kh, qh[ds], s[mb]);
+                    } else {
+                        s[mb] = Op::mma(kh, qh[ds], s[mb]);
+                    }
+                }
+            }
+        };
+
+        f32x16 o[2] = {f32x16{}, f32x16{}};  // O^T: d = 32 db + 8 (i/4) + 4 h + i%4, query q
+        // m_run: the exponent offset of o and l_run (log2 units), always a value
+        // of the operand type. bias_q: the offset the bias operand bq carries,
+        // i.e. the offset of scores computed from now on; bias_cur: that of the
+        // tile being finished (0 for the first tile).
+        float m_run = -INFINITY, l_run = 0.0f, bias_cur = 0.0f, bias_q = 0.0f;
+        V8 bq = bias_b<M>(0.0f, h);
+
+        // One key tile: finish tile t from s_cur (softmax, O^T += V^T P^T) while
+        // tile t + 1's scores go into s_next, interleaved on the matrix cores.
+        auto step = [&](uint32_t t, f32x16 (&s_cur)[2], f32x16 (&s_next)[2]) {
+            const bool more = t + 1 < k1;
+            if (more) {
+                arrive(t + 1);  // also: every wave is past tile t - 1, whose slot is reloaded next
+                if (t + STAGES - 1 < k1) issue(t + STAGES - 1);
+            }
+            // The running max only moves when the tile's max exceeds it by more
+            // than RESCALE; the scores already carry the offset unless it moved
+            // since they were computed.
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) tmax = fmaxf(tmax, s_cur[mb][r]);
+            const float top = max_xor32(tmax) + bias_cur;  // finite: every tile holds a key < T
+            const bool up = top > m_run + RESCALE;
+            if (__any(up)) {
+                const float m_new = up ? representable<M>(top) : m_run;
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
+                o[0] *= alpha;
+                o[1] *= alpha;
+                m_run = m_new;
+                bq = bias_b<M>(m_new, h);
+                bias_q = m_new;
+            }
+            const float shift = m_run - bias_cur;
+            if (__any(shift != 0.0f)) {
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) s_cur[mb][r] -= shift;
+            }
+            bias_cur = bias_q;
+
+            const char *vs = smem + ((t - k0) % STAGES) * STAGE_BYTES + K_BYTES + lrow;
+            float psum = 0.0f;
+            if constexpr (!SPLIT) {
+                // f16: an explicit schedule. The tile's 16 LDS fragments are read
+                // first; then each score product of tile t + 1 is followed by
+                // four of this tile's exponentials, and each value product by
+                // the conversions and row sums that feed the next.
+                typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+                const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+                const char *ks = smem + ((t + 1 - k0) % STAGES) * STAGE_BYTES + lrow;
+                V8 kf[8], vf[8];
+                if (more) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) kf[i] = *(const V8 *)(ks + (i / 4) * 32 * ROWB + (((2 * (i % 4) + h) ^ x) << 4));
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) vf[i] = *(const V8 *)(vs + (i % 2) * 32 * ROWB + (((2 * (i / 2) + h) ^ x) << 4));
+                auto exp4 = [&](int c) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) s_cur[c / 4][4 * (c % 4) + r] = __builtin_amdgcn_exp2f(s_cur[c / 4][4 * (c % 4) + r]);
+                };
+                __builtin_amdgcn_sched_barrier(0);
+                if (more) {
+#pragma unroll
+                    for (int mb = 0; mb < 2; mb++) {
+                        const uint32_t key = (t + 1) * KT + 32 * mb + l32;
+                        s_next[mb] = Op::mma(bias_a<M>(h == 0, key >= Tn), bq, f32x16{});
+                        exp4(mb);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+#pragma unroll
+                    for (int ds = 0; ds < 4; ds++)
+#pragma unroll
+                        for (int mb = 0; mb < 2; mb++) {
+                            s_next[mb] = Op::mma(kf[4 * mb + ds], qh[ds], s_next[mb]);
+                            if (2 + 2 * ds + mb < 8) exp4(2 + 2 * ds + mb);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) exp4(c);
+                }
+#pragma unroll
+                for (int st2 = 0; st2 < 4; st2++) {
+                    const int mb = st2 >> 1, hf = st2 & 1;
+                    V8 ph;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) ph[e] = (_Float16)s_cur[mb][8 * hf + e];
+                    o[0] = Op::mma(vf[2 * st2], ph, o[0]);
+                    psum = __builtin_amdgcn_fdot2(h2{ph[0], ph[1]}, one, psum, false);
+                    psum = __builtin_amdgcn_fdot2(h2{ph[2], ph[3]}, one, psum, false);
+                    __builtin_amdgcn_sched_barrier(0);
+                    o[1] = Op::mma(vf[2 * st2 + 1], ph, o[1]);
+                    psum = __builtin_amdgcn_fdot2(h2{ph[4], ph[5]}, one, psum, false);
+                    psum = __builtin_amdgcn_fdot2(h2{ph[6], ph[7]}, one, psum, false);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            } else {
+                // bf16x3: tile t + 1's scores on the matrix cores while this
+                // tile's probabilities are made on the vector ALUs.
+                if (more) scores(t + 1, bq, s_next);
+#pragma unroll
+                for (int mb = 0; mb < 2; mb++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) s_cur[mb][r] = __builtin_amdgcn_exp2f(s_cur[mb][r]);
+                // O^T += V^T P^T, 16 keys a step: the step's probabilities are
+                // accumulators 8 (st%2) .. +7 of key block st/2, keys 16 st + 4 h + 0..3
+                // and 16 st + 8 + 4 h + 0..3, the order the Vt row holds them in.
+#pragma unroll
+                for (int st2 = 0; st2 < 4; st2++) {
+                    const int mb = st2 >> 1, hf = st2 & 1;
+                    V8 ph, pl;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float p = s_cur[mb][8 * hf + e];
+                        __bf16 hi, lo;
+                        split_bf16(p, hi, lo);
+                        ph[e] = hi;
+                        pl[e] = lo;
+                        psum += p;
+                    }
+#pragma unroll
+                    for (int db = 0; db < 2; db++) {
+                        const int off = db * 32 * ROWB + (((2 * st2 + h) ^ x) << 4);
+                        const V8 vh = *(const V8 *)(vs + off);
+                        const V8 vl = *(const V8 *)(vs + TILE_BYTES + off);
+                        o[db] = Op::mma(vl, ph, o[db]);
+                        o[db] = Op::mma(vh, pl, o[db]);
+                        o[db] = Op::mma(vh, ph, o[db]);
+                    }
+                }
+            }
+            l_run += psum;
+            asm volatile("" ::: "memory");
+        };
+
+        for (uint32_t t = k0; t < k0 + STAGES - 1 && t < k1; t++) issue(t);
+        arrive(k0);
+        f32x16 sa[2], sb[2];
+        scores(k0, bq, sa);
+        uint32_t t = k0;
+        for (; t + 1 < k1; t += 2) {
+            step(t, sa, sb);
+            step(t + 1, sb, sa);
+        }
+        if (t < k1) step(t, sa, sb);
+
+        // The segment's result: the output itself when it covered every key
+        // tile, else (max, sum, unnormalised output) in the run's slot.
+        const float l_tot = sum_xor32(l_run);
+        if (q < args.row1) {
+            if (k0 == 0 && k1 == kt) {
+                const float inv = 1.0f / l_tot;
+                T *out = (T *)args.out + ((uint64_t)q * H + head) * HD;
+#pragma unroll
+                for (int db = 0; db < 2; db++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int d = 32 * db + 8 * j + 4 * h;
+                        if constexpr (SPLIT) {
+                            *(f32x4 *)(out + d) = f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]} * inv;
+                        } else {
+                            f16x4 w;
+#pragma unroll
+                            for (int r = 0; r < 4; r++) w[r] = (_Float16)(o[db][4 * j + r] * inv);
+                            *(f16x4 *)(out + d) = w;
+                        }
+                    }
+            } else {
+                const uint64_t row = ((uint64_t)v * 2 + (first ? 0 : 1)) * QROWS + wave * 32 + l32;
+                float *part = args.partial + row * HD;
+#pragma unroll
+                for (int db = 0; db < 2; db++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        *(f32x4 *)(part + 32 * db + 8 * j + 4 * h) =
+                            f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
+                if (h == 0) *(f32x2 *)(args.stats + 2 * row) = f32x2{m_run, l_tot};
+            }
+        }
+        u += k1 - k0;
+        first = false;
+        // Every wave is done with the ring before the next segment refills it,
+        // and no store is left outstanding under the next segment's load counts.
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
+}
+
+// Combines the partial results of the query tiles whose key tiles were spread
+// over more than one run: O = sum_r 2^(m_r - m) O_r / sum_r 2^(m_r - m) l_r,
+// folded run by run with a running max. A workgroup takes 16 rows of one
+// (head, query tile); one invocation per (row, 4 columns).
+constexpr uint32_t MERGE_ROWS = 16;
+template <Math M>
+__global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
+    using T = typename FlashTraits<M>::T;
+    constexpr uint32_t QROWS = query_rows<M>();
+    const uint32_t item = blockIdx.x / (QROWS / MERGE_ROWS);
+    const uint32_t r = (blockIdx.x % (QROWS / MERGE_ROWS)) * MERGE_ROWS + threadIdx.x / (HD / 4);
+    const uint32_t d = (threadIdx.x % (HD / 4)) * 4;
+    const uint32_t kt = a.t_pad / KT, H = a.heads;
+    const uint32_t U = a.units, G = a.wgs;
+    const uint32_t u0 = item * kt;
+    const uint32_t vf = run_of(u0, U, G), vl = run_of(u0 + kt - 1, U, G);
+    if (vf == vl) return;  // one run held the whole tile: written by attn_kernel
+    const uint32_t head = item / a.qtiles, qt = item % a.qtiles;
+    const uint32_t q = a.row0 + qt * QROWS + r;
+    if (q >= a.row1) return;
+    // The first run holds this tile in its second slot unless the run starts with it.
+    const uint32_t first_slot = run_begin(vf, U, G) < u0 ? 1 : 0;
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0, 0, 0, 0};
+    for (uint32_t v = vf; v <= vl; v++) {
+        const uint64_t row = ((uint64_t)v * 2 + (v == vf ? first_slot : 0)) * QROWS + r;
+        const f32x2 st = *(const f32x2 *)(a.stats + 2 * row);
+        const f32x4 ov = *(const f32x4 *)(a.partial + row * HD + d);
+        const float m_new = fmaxf(m, st[0]);
+        const float wa = __builtin_amdgcn_exp2f(m - m_new), wb = __builtin_amdgcn_exp2f(st[0] - m_new);
+        l = l * wa + st[1] * wb;
+        acc = acc * wa + ov * wb;
+        m = m_new;
+    }
+    const float inv = 1.0f / l;
+    T *out = (T *)a.out + ((uint64_t)q * H + head) * HD + d;
+    if constexpr (M == Math::SPLIT) {
+        *(f32x4 *)out = acc * inv;
+    } else {
+        f16x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = (_Float16)(acc[e] * inv);
+        *(f16x4 *)out = w;
+    }
+}
+
+// ---- 3. the 16 x 16 kernel (f32 math) ----
+__global__ __launch_bounds__(THREADS) void flash16_kernel(FlashArgs args) {
+    using Tr = FlashTraits<Math::F32>;
+    constexpr int CPR = Tr::CPR, STAGES = Tr::STAGES;
+    constexpr int TILE_BYTES = 64 * CPR * 16;
+    constexpr int K_BYTES = TILE_BYTES;
+    constexpr int STAGE_BYTES = 2 * K_BYTES;
+    constexpr int LPS = 2 * loads_per_wave<64, CPR>();
+
+    __shared__ __attribute__((aligned(16))) char smem[STAGES * STAGE_BYTES];
+
+    const float *__restrict__ qkv = (const float *)args.qkv;
     const uint32_t Tn = args.tokens, H = args.heads, tpad = args.t_pad;
     const uint32_t row_stride = 3 * H * HD;
     const uint32_t head = blockIdx.y, split = blockIdx.z;
@@ -159,67 +600,30 @@ __global__ __launch_bounds__(THREADS) void flash_kernel(FlashArgs args) {
     const uint32_t t_begin = split * ntiles / args.splits;
     const uint32_t t_end = (split + 1) * ntiles / args.splits;
 
-    // This head's K [tpad][64] and Vt [64][tpad], per plane.
-    constexpr int ESZ = sizeof(L);
-    const uint64_t plane_bytes = (uint64_t)H * tpad * HD * ESZ;
+    constexpr int ESZ = 4;
     const char *kbase = (const char *)args.kp + (uint64_t)head * tpad * HD * ESZ;
     const char *vbase = (const char *)args.vt + (uint64_t)head * HD * tpad * ESZ;
-
     const RowLoader<64, CPR> kload(HD * ESZ, 63, wave, lane);
     const RowLoader<64, CPR> vload(tpad * ESZ, 63, wave, lane);
     auto issue = [&](uint32_t t, int slot) {
         char *st = smem + slot * STAGE_BYTES;
-#pragma unroll
-        for (int p = 0; p < PLANES; p++) {
-            // K rows: 64 keys of 64 d; Vt rows: 64 d of 64 keys, from key t*64.
-            kload.issue(kbase + p * plane_bytes + (uint64_t)t * KT * HD * ESZ, st + p * TILE_BYTES);
-            vload.issue(vbase + p * plane_bytes + (uint64_t)t * KT * ESZ, st + K_BYTES + p * TILE_BYTES);
-        }
+        kload.issue(kbase + (uint64_t)t * KT * HD * ESZ, st);
+        vload.issue(vbase + (uint64_t)t * KT * ESZ, st + K_BYTES);
     };
 
-    // Fragment offsets inside a staged tile: row 16 j + l16 has the same
-    // swizzle for every j, so only the lane's own part is computed here.
-    constexpr int ROWB = CPR * 16;  // bytes per staged row
+    constexpr int ROWB = CPR * 16;
     const int lrow = l16 * ROWB;
-    const int x = (CPR == 16) ? l16 : ((l16 >> 1) & 7);
+    const int x = l16;
 
-    // ---- the wave's queries as the B operand of S^T = K Q^T ----
-    const T *qrow = qkv + (uint64_t)q * row_stride + head * HD;
-    f16x8 qf16[2];
-    bf16x8 qhi[2], qlo[2];
+    // Step (h, s) of the 16 x 16 x 4 products: lane group g reads d = 16h + 4g + s.
+    const float *qrow = qkv + (uint64_t)q * row_stride + head * HD;
     float qf32[16];
-    if constexpr (M == Math::F16) {
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            f16x8 v = {};
-            if (q_ok) v = *(const f16x8 *)(qrow + 32 * c + 8 * g);
-            qf16[c] = v;
-        }
-    } else if constexpr (M == Math::SPLIT) {
+    for (int hh = 0; hh < 4; hh++) {
+        f32x4 a = {};
+        if (q_ok) a = *(const f32x4 *)(qrow + 16 * hh + 4 * g);
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            f32x4 a = {}, b = {};
-            if (q_ok) {
-                a = *(const f32x4 *)(qrow + 32 * c + 8 * g);
-                b = *(const f32x4 *)(qrow + 32 * c + 8 * g + 4);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                __bf16 h, l;
-                split_bf16(e < 4 ? a[e] : b[e - 4], h, l);
-                qhi[c][e] = h;
-                qlo[c][e] = l;
-            }
-        }
-    } else {
-        // Step (h, s) of the 16 x 16 x 4 products: lane group g reads d = 16h + 4g + s.
-#pragma unroll
-        for (int h = 0; h < 4; h++) {
-            f32x4 a = {};
-            if (q_ok) a = *(const f32x4 *)(qrow + 16 * h + 4 * g);
-#pragma unroll
-            for (int s = 0; s < 4; s++) qf32[4 * h + s] = a[s];
-        }
+        for (int s = 0; s < 4; s++) qf32[4 * hh + s] = a[s];
     }
 
     f32x4 o[4];  // O^T: d = 16 dt + 4g + r, query l16
@@ -242,68 +646,35 @@ __global__ __launch_bounds__(THREADS) void flash_kernel(FlashArgs args) {
         const char *st = smem + (i % STAGES) * STAGE_BYTES;
         const char *ks = st, *vs = st + K_BYTES;
 
-        // S^T tiles: keys 16 kt + 4g + r of this tile, query l16.
         f32x4 s[4];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++) {
             f32x4 acc = {0, 0, 0, 0};
             const char *krow = ks + kt * 16 * ROWB + lrow;
-            if constexpr (M == Math::F16) {
 #pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    f16x8 a = *(const f16x8 *)(krow + (((4 * c + g) ^ x) << 4));
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf16[c], acc, 0, 0, 0);
-                }
-            } else if constexpr (M == Math::SPLIT) {
+            for (int hh = 0; hh < 4; hh++) {
+                f32x4 a = *(const f32x4 *)(krow + (((4 * hh + g) ^ x) << 4));
 #pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    const int off = ((4 * c + g) ^ x) << 4;
-                    bf16x8 ah = *(const bf16x8 *)(krow + off);
-                    bf16x8 al = *(const bf16x8 *)(krow + TILE_BYTES + off);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, qhi[c], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qlo[c], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, qhi[c], acc, 0, 0, 0);
-                }
-            } else {
-#pragma unroll
-                for (int h = 0; h < 4; h++) {
-                    f32x4 a = *(const f32x4 *)(krow + (((4 * h + g) ^ x) << 4));
-#pragma unroll
-                    for (int st2 = 0; st2 < 4; st2++)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st2], qf32[4 * h + st2], acc, 0, 0, 0);
-                }
+                for (int st2 = 0; st2 < 4; st2++)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st2], qf32[4 * hh + st2], acc, 0, 0, 0);
             }
             s[kt] = acc;
         }
 
-        // Online softmax for query l16 over this tile's keys; only a tile
-        // reaching past the last token masks.
         const uint32_t kb = t * KT;
         float tmax = -INFINITY;
-        if (kb + KT <= Tn) {
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++)
+        for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    s[kt][r] *= sl2;
-                    tmax = fmaxf(tmax, s[kt][r]);
-                }
-        } else {
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint32_t key = kb + 16 * kt + 4 * g + r;
-                    const float v = key < Tn ? s[kt][r] * sl2 : -INFINITY;
-                    s[kt][r] = v;
-                    tmax = fmaxf(tmax, v);
-                }
-        }
+            for (int r = 0; r < 4; r++) {
+                const uint32_t key = kb + 16 * kt + 4 * g + r;
+                const float v = key < Tn ? s[kt][r] * sl2 : -INFINITY;
+                s[kt][r] = v;
+                tmax = fmaxf(tmax, v);
+            }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);  // finite: every tile has a key < T
-        // 2^x on v_exp_f32: arguments are <= 0, results in (0, 1]; an
-        // underflow to zero is a probability below 2^-126.
+        const float m_new = fmaxf(m_run, tmax);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
         float psum = 0.0f;
@@ -319,89 +690,29 @@ __global__ __launch_bounds__(THREADS) void flash_kernel(FlashArgs args) {
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) o[dt] *= alpha;
 
-        // O^T += V^T P^T.
-        if constexpr (M == Math::F32) {
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                const char *vrow = vs + dt * 16 * ROWB + lrow;
+        for (int dt = 0; dt < 4; dt++) {
+            const char *vrow = vs + dt * 16 * ROWB + lrow;
 #pragma unroll
-                for (int kt = 0; kt < 4; kt++) {
-                    f32x4 a = *(const f32x4 *)(vrow + (((4 * kt + g) ^ x) << 4));
+            for (int kt = 0; kt < 4; kt++) {
+                f32x4 a = *(const f32x4 *)(vrow + (((4 * kt + g) ^ x) << 4));
 #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], s[kt][r], o[dt], 0, 0, 0);
-                }
-            }
-        } else {
-            // 32 keys per step: slots 0..3 are keys 32m + 4g + e, slots 4..7 keys
-            // 32m + 16 + 4g + e, for A (V^T) and B (P^T) alike.
-#pragma unroll
-            for (int mh = 0; mh < 2; mh++) {
-                // The 4-key runs at 32mh + 4g and 32mh + 16 + 4g: chunks
-                // 4mh + g/2 and 4mh + 2 + g/2, half (g & 1) of each.
-                const int o0 = (((4 * mh + (g >> 1)) ^ x) << 4) + (g & 1) * 8;
-                const int o1 = (((4 * mh + 2 + (g >> 1)) ^ x) << 4) + (g & 1) * 8;
-                if constexpr (M == Math::F16) {
-                    f16x8 b;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        b[e] = (_Float16)s[2 * mh][e];
-                        b[4 + e] = (_Float16)s[2 * mh + 1][e];
-                    }
-#pragma unroll
-                    for (int dt = 0; dt < 4; dt++) {
-                        const char *vrow = vs + dt * 16 * ROWB + lrow;
-                        const f16x4 lo = *(const f16x4 *)(vrow + o0);
-                        const f16x4 hi = *(const f16x4 *)(vrow + o1);
-                        const f16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, o[dt], 0, 0, 0);
-                    }
-                } else {
-                    bf16x8 bh, bl;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        __bf16 h, l;
-                        split_bf16(e < 4 ? s[2 * mh][e] : s[2 * mh + 1][e - 4], h, l);
-                        bh[e] = h;
-                        bl[e] = l;
-                    }
-#pragma unroll
-                    for (int dt = 0; dt < 4; dt++) {
-                        const char *vrow = vs + dt * 16 * ROWB + lrow;
-                        const bf16x4 h0 = *(const bf16x4 *)(vrow + o0), h1 = *(const bf16x4 *)(vrow + o1);
-                        const bf16x4 l0 = *(const bf16x4 *)(vrow + TILE_BYTES + o0), l1 = *(const bf16x4 *)(vrow + TILE_BYTES + o1);
-                        const bf16x8 ah = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-                        const bf16x8 al = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, o[dt], 0, 0, 0);
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, o[dt], 0, 0, 0);
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, o[dt], 0, 0, 0);
-                    }
-                }
+                for (int r = 0; r < 4; r++)
+                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], s[kt][r], o[dt], 0, 0, 0);
             }
         }
         asm volatile("" ::: "memory");
     }
 
-    // The row sum over the four lane groups of query l16.
     l_run += __shfl_xor(l_run, 16, 64);
     l_run += __shfl_xor(l_run, 32, 64);
     if (!q_ok) return;
 
     if (args.splits == 1) {
         const float inv = 1.0f / l_run;
-        T *out = (T *)args.out + (uint64_t)q * H * HD + head * HD;
+        float *out = (float *)args.out + (uint64_t)q * H * HD + head * HD;
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-            const int d = 16 * dt + 4 * g;
-            if constexpr (M == Math::F16) {
-                f16x4 v;
-#pragma unroll
-                for (int r = 0; r < 4; r++) v[r] = (_Float16)(o[dt][r] * inv);
-                *(f16x4 *)(out + d) = v;
-            } else {
-                *(f32x4 *)(out + d) = o[dt] * inv;
-            }
-        }
+        for (int dt = 0; dt < 4; dt++) *(f32x4 *)(out + 16 * dt + 4 * g) = o[dt] * inv;
     } else {
         const uint64_t slot = ((uint64_t)split * Tn + q) * H + head;
         float *part = args.partial + slot * HD;
@@ -411,11 +722,7 @@ __global__ __launch_bounds__(THREADS) void flash_kernel(FlashArgs args) {
     }
 }
 
-// ---- 3. merging the key splits ----
-// O = sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s, one invocation per
-// (query, head, 4 output columns).
-template <typename T>
-__global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs args) {
+__global__ __launch_bounds__(256) void flash16_merge_kernel(FlashArgs args) {
     const uint32_t H = args.heads, Tn = args.tokens;
     const uint64_t per_row = (uint64_t)H * (HD / 4);
     const uint64_t total = (uint64_t)(args.row1 - args.row0) * per_row;
@@ -424,42 +731,54 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(FlashArgs args) {
         const uint32_t q = args.row0 + (uint32_t)(i / per_row);
         const uint32_t rem = (uint32_t)(i % per_row);
         const uint32_t head = rem / (HD / 4), d = (rem % (HD / 4)) * 4;
-        f32x2 st[8];
         float m = -INFINITY;
-        for (uint32_t s = 0; s < args.splits; s++) {
-            st[s] = *(const f32x2 *)(args.stats + 2 * (((uint64_t)s * Tn + q) * H + head));
-            m = fmaxf(m, st[s][0]);
-        }
+        for (uint32_t s = 0; s < args.splits; s++)
+            m = fmaxf(m, args.stats[2 * (((uint64_t)s * Tn + q) * H + head)]);
         f32x4 acc = {0, 0, 0, 0};
         float l = 0.0f;
         for (uint32_t s = 0; s < args.splits; s++) {
-            if (st[s][0] == -INFINITY) continue;  // a split with no keys
             const uint64_t slot = ((uint64_t)s * Tn + q) * H + head;
-            const float w = exp2f(st[s][0] - m);
-            l += w * st[s][1];
+            const float w = exp2f(args.stats[2 * slot] - m);
+            l += w * args.stats[2 * slot + 1];
             acc += w * *(const f32x4 *)(args.partial + slot * HD + d);
         }
         const float inv = 1.0f / l;
-        T *out = (T *)args.out + (uint64_t)q * H * HD + head * HD + d;
-#pragma unroll
-        for (int r = 0; r < 4; r++) out[r] = from_f32<T>(acc[r] * inv);
+        float *out = (float *)args.out + (uint64_t)q * H * HD + head * HD + d;
+        *(f32x4 *)out = acc * inv;
     }
 }
 
+constexpr uint32_t FLASH16_MAX_SPLITS = 8;
+
+uint64_t operand_bytes(Math m, uint32_t heads, uint32_t t_pad) {
+    const uint64_t per = (uint64_t)heads * t_pad * HD;
+    return 2 * per * (m == Math::F16 ? 2 : 4);  // K and Vt; SPLIT's two bf16 planes are 4 bytes together
+}
+
 template <Math M>
-hipError_t launch_m(const FlashArgs &a, hipStream_t s) {
-    using T = typename FlashTraits<M>::T;
-    hipLaunchKernelGGL(flash_prep_kernel<M>, dim3(a.t_pad / KT, a.heads), dim3(THREADS), 0, s, a);
+hipError_t launch_32(const FlashArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((flash_prep_kernel<M, true>), dim3(a.t_pad / KT, a.heads), dim3(THREADS), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attn_kernel<M>, dim3(a.wgs), dim3(THREADS32), 0, s, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || !a.merge) return e;
+    const uint32_t blocks = a.qtiles * a.heads * (query_rows<M>() / MERGE_ROWS);
+    hipLaunchKernelGGL(attn_merge_kernel<M>, dim3(blocks), dim3(MERGE_ROWS * (HD / 4)), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_16(const FlashArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL((flash_prep_kernel<Math::F32, false>), dim3(a.t_pad / KT, a.heads), dim3(THREADS), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     dim3 grid((a.row1 - a.row0 + 63) / 64, a.heads, a.splits);
-    hipLaunchKernelGGL(flash_kernel<M>, grid, dim3(THREADS), 0, s, a);
+    hipLaunchKernelGGL(flash16_kernel, grid, dim3(THREADS), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess || a.splits == 1) return e;
     uint64_t work = (uint64_t)(a.row1 - a.row0) * a.heads * (HD / 4);
-    uint32_t blocks = (uint32_t)((work + 255) / 256);
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(flash_merge_kernel<T>, dim3(blocks), dim3(256), 0, s, a);
+    uint32_t blocks = (uint32_t)std::min<uint64_t>((work + 255) / 256, 4096);
+    hipLaunchKernelGGL(flash16_merge_kernel, dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -468,15 +787,58 @@ hipError_t launch_m(const FlashArgs &a, hipStream_t s) {
 hipError_t launch_flash(const FlashArgs &a, Math m, hipStream_t s) {
     if (a.row1 <= a.row0) return hipSuccess;
     switch (m) {
-    case Math::F16: return launch_m<Math::F16>(a, s);
-    case Math::SPLIT: return launch_m<Math::SPLIT>(a, s);
-    default: return launch_m<Math::F32>(a, s);
+    case Math::F16: return launch_32<Math::F16>(a, s);
+    case Math::SPLIT: return launch_32<Math::SPLIT>(a, s);
+    default: return launch_16(a, s);
     }
 }
 
-uint64_t flash_operand_bytes(Math m, uint32_t heads, uint32_t t_pad) {
-    const uint64_t per = (uint64_t)heads * t_pad * HD;
-    return 2 * per * (m == Math::F16 ? 2 : 4);  // K and Vt; SPLIT's two bf16 planes are 4 bytes together
+FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uint32_t row1, uint32_t compute_units) {
+    FlashPlan p;
+    const uint32_t rows = row1 > row0 ? row1 - row0 : 0;
+    const uint32_t t_pad = (tokens + KT - 1) / KT * KT;
+    const uint32_t kt = t_pad / KT;
+    uint64_t extra = 0;
+    if (m == Math::F32) {
+        const uint32_t wgs = (rows + 63) / 64 * heads;
+        // Enough workgroups for two per CU, each split keeping two key tiles or more.
+        uint32_t splits = wgs ? (2 * compute_units + wgs - 1) / wgs : 1;
+        p.splits = std::max<uint32_t>(1, std::min<uint32_t>({splits, kt / 2, FLASH16_MAX_SPLITS}));
+        if (p.splits > 1) extra = (uint64_t)p.splits * tokens * heads * (HD + 2) * sizeof(float);
+    } else {
+        const uint32_t qrows = m == Math::F16 ? query_rows<Math::F16>() : query_rows<Math::SPLIT>();
+        p.qtiles = (rows + qrows - 1) / qrows;
+        p.units = (uint64_t)heads * p.qtiles * kt;
+        // One workgroup per CU (its 8 waves are two per SIMD).
+        const uint64_t slots = std::max<uint32_t>(compute_units, 1);
+        p.wgs = (uint32_t)std::min<uint64_t>(p.units, slots);
+        if (const char *force = getenv("BL_FLASH_RUNS")) {
+            const long w = atol(force);
+            if (w > 0) p.wgs = (uint32_t)std::min<uint64_t>(p.units, (uint64_t)w);
+        }
+        // The run arithmetic is 32-bit.
+        if (p.units * p.wgs >= (1ull << 32)) p.wgs = (uint32_t)(((1ull << 32) - 1) / p.units);
+        for (uint32_t item = 0; item < heads * p.qtiles && !p.merge; item++)
+            p.merge = run_of(item * kt, (uint32_t)p.units, p.wgs) != run_of(item * kt + kt - 1, (uint32_t)p.units, p.wgs);
+        // Two result slots per run: its first and its last segment.
+        extra = (uint64_t)p.wgs * 2 * qrows * (HD + 2) * sizeof(float);
+    }
+    p.scratch_bytes = operand_bytes(m, heads, t_pad) + extra;
+    return p;
+}
+
+void bind_flash_scratch(FlashArgs &a, Math m, void *base) {
+    const uint64_t ops = operand_bytes(m, a.heads, a.t_pad);
+    char *b = (char *)base;
+    a.kp = b;
+    a.vt = b + ops / 2;
+    a.partial = (float *)(b + ops);
+    if (m == Math::F32) {
+        a.stats = a.partial + (uint64_t)a.splits * a.tokens * a.heads * HD;
+    } else {
+        const uint32_t qrows = m == Math::F16 ? query_rows<Math::F16>() : query_rows<Math::SPLIT>();
+        a.stats = a.partial + (uint64_t)a.wgs * 2 * qrows * HD;
+    }
 }
 
 }  // namespace bl

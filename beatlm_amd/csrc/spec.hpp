@@ -84,12 +84,25 @@ struct FlashArgs {
     void *out;
     void *kp;             // keys [planes][heads][t_pad][64] in the operand type
     void *vt;             // values transposed [planes][heads][64][t_pad]
-    float *partial;       // [splits][tokens][heads][64] f32, when splits > 1
-    float *stats;         // [splits][tokens][heads][2] (max, sum), when splits > 1
+    float *partial;       // partial outputs of key ranges (unnormalised, f32)
+    float *stats;         // their (max, sum) pairs
     uint32_t tokens, heads, t_pad;
     uint32_t row0, row1;  // query rows of the part
-    uint32_t splits;
+    uint32_t splits;      // f32 math: key ranges per query tile
     float scale;          // softmax scale (the Scale epilogue of the scores)
+    // f16 and bf16x3 math: the (head, query tile, key tile) units are dealt
+    // out in equal contiguous runs to `wgs` workgroups.
+    uint32_t qtiles, wgs;
+    uint64_t units;
+    uint32_t merge;       // 1 when some query tile's key tiles span two runs
+};
+
+// How a flash attention spec is launched: its grid and the scratch it needs
+// (operands, then partial outputs and statistics).
+struct FlashPlan {
+    uint32_t splits = 1, qtiles = 0, wgs = 0, merge = 0;
+    uint64_t units = 0;
+    uint64_t scratch_bytes = 0;
 };
 
 // One element per invocation: the standalone map, the token copies.
@@ -127,9 +140,9 @@ inline uint64_t packed_bytes(Math m, uint32_t k_pad, uint32_t n_pad) {
 hipError_t launch_gather(const GatherArgs &a, Gather g, bool f16, hipStream_t s);
 hipError_t launch_softmax(const SoftmaxArgs &a, bool f16, hipStream_t s);
 hipError_t launch_flash(const FlashArgs &a, Math m, hipStream_t s);
-uint64_t flash_operand_bytes(Math m, uint32_t heads, uint32_t t_pad);
-// The most key splits the merge takes.
-constexpr uint32_t FLASH_MAX_SPLITS = 8;
+FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uint32_t row1, uint32_t compute_units);
+// Points a planned FlashArgs at its scratch (plan.scratch_bytes at `base`).
+void bind_flash_scratch(FlashArgs &a, Math m, void *base);
 hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s);
 hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
 
@@ -140,8 +153,6 @@ inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64}; return c[t
 // K and N of a packed B are padded to these.
 constexpr uint32_t PACK_K = 32, PACK_N = 128;
 
-// The flash kernel's query rows per workgroup.
-constexpr uint32_t FLASH_ROWS = 64;
 constexpr uint32_t FLASH_HEAD_DIM = 64;
 
 }  // namespace bl

@@ -38,6 +38,7 @@ struct Slot {
 
 struct bl_timer {
     bl_ctx *ctx = nullptr;
+    bool retained = false;         // holds a reference on ctx (set once created)
     uint32_t max_slices = 0;
     std::vector<Slot> slots;
     int open = -1;                 // slot of the frame being recorded, -1 when untimed
@@ -79,6 +80,8 @@ extern "C" int bl_timer_create(bl_ctx *ctx, uint32_t max_slices, bl_timer **out)
         created++;
     }
     bl_events_counted(ctx, created);
+    bl_ctx_retain(ctx);
+    t->retained = true;
     *out = t;
     return BL_OK;
 }
@@ -91,7 +94,9 @@ extern "C" void bl_timer_destroy(bl_timer *t) {
             if (e) hipEventDestroy(e);
         if (s.done) hipEventDestroy(s.done);
     }
+    bl_ctx *ctx = t->retained ? t->ctx : nullptr;
     delete t;
+    if (ctx) bl_ctx_release(ctx);
 }
 
 extern "C" int bl_timer_begin_frame(bl_timer *t, uint64_t frame, uint32_t *timed) {

@@ -191,6 +191,8 @@ typedef struct bl_timer bl_timer;
 /* ---- context ---- */
 uint32_t bl_abi_version(void);
 int bl_ctx_create(int device_ordinal, bl_ctx **out);
+/* Arenas, kernels and timers keep their context alive: destroying the context
+ * first is allowed, and it is released when the last of them is destroyed. */
 void bl_ctx_destroy(bl_ctx *ctx);
 const char *bl_last_error(const bl_ctx *ctx);
 int bl_device_profile(bl_ctx *ctx, bl_device_profile_t *out);
