@@ -441,6 +441,13 @@ uint64_t round4(uint64_t bytes) { return (bytes + 3) / 4 * 4; }
 
 }  // namespace
 
+// A range of kernels captured once as a HIP graph and replayed by
+// bl_kernels_encode_range: one submission instead of one per launch.
+struct RangeGraph {
+    uint32_t first, count, set;
+    hipGraphExec_t exec;
+};
+
 struct bl_kernels {
     bl_ctx *ctx = nullptr;
     bl_arenas *arenas = nullptr;
@@ -449,6 +456,11 @@ struct bl_kernels {
     void *scratch = nullptr;
     std::vector<Pack> packs;
     void *pack_buffer = nullptr;
+    std::vector<RangeGraph> graphs;
+    // Graphs replay fixed launches: not used when a kernel of the program
+    // rewrites a packed weight's source (the pack must rerun in between), or
+    // when BL_NO_GRAPH is set.
+    bool graphs_ok = true;
 };
 
 extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs, uint32_t n,
@@ -656,23 +668,26 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
                     pack = (int)ks->packs.size() - 1;
                 }
                 L.pack = pack;
-                L.gemm = ga;
-                // The largest tile that still gives every CU two workgroups.
                 const uint32_t rows = pt.end - pt.start;
-                const int order[] = {TILE_128x64, TILE_64x128, TILE_64x64, TILE_32x64};
-                int chosen = TILE_32x64;
-                for (int t : order) {
-                    uint64_t wgs = (uint64_t)((rows + gemm_tile_rows(t) - 1) / gemm_tile_rows(t)) *
-                                   ((gn + gemm_tile_cols(t) - 1) / gemm_tile_cols(t));
-                    if (wgs >= 2ull * ctx->compute_units) { chosen = t; break; }
-                }
+                auto wgs_of = [&](int t) {
+                    return (uint64_t)((rows + gemm_tile_rows(t) - 1) / gemm_tile_rows(t)) *
+                           ((gn + gemm_tile_cols(t) - 1) / gemm_tile_cols(t));
+                };
+                // 64 x 64 tiles when they fill every CU in one round (two
+                // workgroups per CU at most), else 32 x 64: at the encoder's
+                // sizes the smaller tile's extra workgroups hide its per-step
+                // waits better than a second round or idle CUs would.
+                const uint64_t w64 = wgs_of(TILE_64x64);
+                int chosen = (w64 >= ctx->compute_units && w64 <= 2ull * ctx->compute_units) ? TILE_64x64 : TILE_32x64;
                 if (const char *force = getenv("BL_GEMM_TILE")) {
                     int t = atoi(force);
                     if (t >= 0 && t < TILE_COUNT) chosen = t;
                 }
+                L.gemm = ga;
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
-                          " " + std::to_string(gemm_tile_rows(chosen)) + "x" + std::to_string(gemm_tile_cols(chosen));
+                          " " + std::to_string(gemm_tile_rows(chosen)) + "x" +
+                          std::to_string(gemm_tile_cols(chosen));
                 break;
             }
             case BL_MAIN_ATTENTION_SCORES:
@@ -754,6 +769,8 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
                     pk.dynamic = true;
             }
         }
+        for (const Pack &pk : ks->packs)
+            if (pk.dynamic) ks->graphs_ok = false;
         ks->pack_buffer = bl_device_alloc(ctx, total);
         if (!ks->pack_buffer) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of packed weights", (unsigned long long)total);
         for (Kernel &k : ks->kernels)
@@ -767,7 +784,42 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
         // uses the same scratch: operands, then partial outputs and statistics.
         for (auto [ki, si] : flash_users)
             bind_flash_scratch(ks->kernels[ki].per_set[si].fl, ks->kernels[ki].per_set[si].math, ks->scratch);
+        // Zeroed once: the operands' padding keys (past the last token) are
+        // never written by a fused QKV projection and must stay finite.
+        if (hipMemset(ks->scratch, 0, scratch_bytes) != hipSuccess)
+            return bad(BL_ERR_HIP, "clearing %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
+        // A flash kernel (f16 or bf16x3) whose qkv comes straight from QKV
+        // projection kernels (no epilogue steps) gets its K and Vt from their
+        // epilogues and skips its own prep launch. Parts of the flash kernel
+        // reading the same qkv share the producers.
+        if (!getenv("BL_NO_FUSED_PREP")) {
+            for (auto [ki, si] : flash_users) {
+                Launch &F = ks->kernels[ki].per_set[si];
+                if (F.math == Math::F32) continue;
+                std::vector<size_t> producers;
+                bool ok = true;
+                for (size_t j = ki; j-- > 0;) {
+                    Launch &P = ks->kernels[j].per_set[si];
+                    if (P.family == Family::FLASH && P.fl.qkv == F.fl.qkv) continue;
+                    if (P.family != Family::GEMM || P.gemm.c != F.fl.qkv) break;
+                    if (P.gemm.load != 0 || P.gemm.epi_mode != 0 || P.math != F.math || P.gemm.m != F.fl.tokens ||
+                        P.gemm.n != 3 * F.fl.heads * FLASH_HEAD_DIM)
+                        ok = false;
+                    producers.push_back(j);
+                }
+                if (!ok || producers.empty()) continue;
+                for (size_t j : producers) {
+                    GemmArgs &ga = ks->kernels[j].per_set[si].gemm;
+                    ga.flash_ops = 1;
+                    ga.fl_kp = F.fl.kp;
+                    ga.fl_vt = F.fl.vt;
+                    ga.fl_tpad = F.fl.t_pad;
+                }
+                F.fl.prepped = 1;
+            }
+        }
     }
+    if (getenv("BL_NO_GRAPH")) ks->graphs_ok = false;
     bl_ctx_retain(ctx);
     *out = ks;
     return BL_OK;
@@ -777,6 +829,7 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
     if (!k) return;
     hipSetDevice(k->ctx->device);
     hipStreamSynchronize(k->ctx->stream);
+    for (RangeGraph &g : k->graphs) hipGraphExecDestroy(g.exec);
     if (k->scratch) hipFree(k->scratch);
     if (k->pack_buffer) hipFree(k->pack_buffer);
     bl_ctx *ctx = k->ctx;
@@ -830,15 +883,55 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
     return BL_OK;
 }
 
+// The range's launches captured on the context's stream, or null when the
+// capture failed (the caller then launches one by one).
+static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set) {
+    hipStream_t s = k->ctx->stream;
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return nullptr;
+    hipError_t e = hipSuccess;
+    for (uint32_t i = first; i < first + count && e == hipSuccess; i++) e = launch(k->kernels[i].per_set[set], s);
+    hipGraph_t g = nullptr;
+    const hipError_t end = hipStreamEndCapture(s, &g);
+    hipGraphExec_t exec = nullptr;
+    if (e == hipSuccess && end == hipSuccess && g) {
+        if (hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) exec = nullptr;
+    }
+    if (g) hipGraphDestroy(g);
+    (void)hipGetLastError();
+    return exec;
+}
+
 extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set) {
     if (!k) return BL_ERR_INVALID_ARGUMENT;
     if ((uint64_t)first + count > k->kernels.size())
         return fail(k->ctx, BL_ERR_NO_SUCH_KERNEL, "there is no kernel %u", first + count - 1);
     if (set >= k->sets) return fail(k->ctx, BL_ERR_NO_SUCH_SET, "there is no binding set %u", set);
+    hipStream_t s = k->ctx->stream;
+    if (k->graphs_ok && count > 1) {
+        // Stale packs are remade first, outside the graph (the graph holds the
+        // program's own launches only).
+        for (uint32_t i = first; i < first + count; i++) {
+            const Launch &L = k->kernels[i].per_set[set];
+            hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
+            if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
+        }
+        hipGraphExec_t exec = nullptr;
+        for (const RangeGraph &g : k->graphs)
+            if (g.first == first && g.count == count && g.set == set) exec = g.exec;
+        if (!exec) {
+            exec = capture_range(k, first, count, set);
+            if (exec) k->graphs.push_back({first, count, set, exec});
+            else k->graphs_ok = false;
+        }
+        if (exec) {
+            hipError_t e = hipGraphLaunch(exec, s);
+            return e == hipSuccess ? BL_OK : hip_fail(k->ctx, e, "graph launch");
+        }
+    }
     for (uint32_t i = first; i < first + count; i++) {
         const Launch &L = k->kernels[i].per_set[set];
-        hipError_t e = L.pack >= 0 ? refresh_pack(k, L, k->ctx->stream) : hipSuccess;
-        if (e == hipSuccess) e = launch(L, k->ctx->stream);
+        hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
+        if (e == hipSuccess) e = launch(L, s);
         if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
     }
     return BL_OK;

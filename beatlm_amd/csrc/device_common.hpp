@@ -43,6 +43,13 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// ---- the attention's value operand layout ----
+// Position of key k inside a row of the transposed values Vt for the 32 x 32
+// flash kernel: bits 2 and 3 of k swapped, so each 16-key group is stored in
+// the order 0-3, 8-11, 4-7, 12-15 in which that kernel's probabilities come
+// out of its score accumulators.
+__host__ __device__ constexpr uint32_t vt_pos(uint32_t k) { return (k & ~12u) | ((k & 4u) << 1) | ((k & 8u) >> 1); }
+
 // ---- lane l and lane l ^ 32 (v_permlane32_swap: no LDS round trip) ----
 // The swap exchanges lanes 32-63 of its first operand with lanes 0-31 of its
 // second; with v in both, the two results hold (v[l], v[l ^ 32]) in some order.

@@ -11,6 +11,8 @@
 //  1. flash_prep_kernel writes the keys as K [H][T_pad][64] and the values
 //     transposed as Vt [H][64][T_pad], once, in the matrix cores' operand type
 //     (f16, f32, or hi and lo bf16 planes), zero-padded to whole 64-key tiles.
+//     When the qkv tensor comes straight from a QKV projection, that GEMM's
+//     epilogue writes these operands instead and this launch is skipped.
 //     For the 32 x 32 kernel each 16-key group of a Vt row is stored in the
 //     order 0-3, 8-11, 4-7, 12-15 (bits 2 and 3 of the key swapped), which is
 //     the order in which that kernel's probabilities come out of its score
@@ -78,9 +80,6 @@ template <> struct FlashTraits<Math::F32> {
 
 // Query rows of one unit (a workgroup's tile) of the 32 x 32 kernel.
 template <Math M> constexpr uint32_t query_rows() { return NW * FlashTraits<M>::QB * 32; }
-
-// Position of key k inside its Vt row for the 32 x 32 kernel: bits 2 and 3 swapped.
-__host__ __device__ constexpr uint32_t vt_pos(uint32_t k) { return (k & ~12u) | ((k & 4u) << 1) | ((k & 8u) >> 1); }
 
 // ---- 1. K and Vt in operand layout ----
 // One workgroup per 64 keys of one head: 16-byte loads of the key and value
@@ -757,9 +756,12 @@ uint64_t operand_bytes(Math m, uint32_t heads, uint32_t t_pad) {
 
 template <Math M>
 hipError_t launch_32(const FlashArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL((flash_prep_kernel<M, true>), dim3(a.t_pad / KT, a.heads), dim3(THREADS), 0, s, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e;
+    if (!a.prepped) {
+        hipLaunchKernelGGL((flash_prep_kernel<M, true>), dim3(a.t_pad / KT, a.heads), dim3(THREADS), 0, s, a);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(attn_kernel<M>, dim3(a.wgs), dim3(THREADS32), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess || !a.merge) return e;

@@ -48,6 +48,12 @@ struct GemmArgs {
     int pipeline;         // 1: the LDS-ring kernel with direct loads (k a multiple of 32)
     uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width
     EpilogueArgs epi;
+    // The QKV projection of a flash attention kernel also writes that
+    // kernel's K [planes][H][t_pad][64] and Vt [planes][H][64][t_pad]
+    // operands (its prep step, fused) when flash_ops is set.
+    int flash_ops;
+    void *fl_kp, *fl_vt;
+    uint32_t fl_tpad;
 };
 
 // B [k][n] -> the GEMM's packed operand (transposed, padded, converted).
@@ -95,6 +101,7 @@ struct FlashArgs {
     uint32_t qtiles, wgs;
     uint64_t units;
     uint32_t merge;       // 1 when some query tile's key tiles span two runs
+    uint32_t prepped;     // 1 when the QKV projection already wrote K and Vt
 };
 
 // How a flash attention spec is launched: its grid and the scratch it needs

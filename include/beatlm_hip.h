@@ -237,7 +237,11 @@ const char *bl_kernels_label(const bl_kernels *kernels, uint32_t kernel);
  * current frame under `tag`. No allocation, no wait. */
 int bl_kernels_encode(bl_kernels *kernels, uint32_t kernel, uint32_t set,
                       bl_timer *timer, uint32_t tag);
-/* Launches kernels [first, first + count) in order with binding set `set`. */
+/* Launches kernels [first, first + count) in order with binding set `set`.
+ * The first call for a (first, count, set) captures the launches as a HIP
+ * graph; later calls replay it (weights packs that went stale since are
+ * remade first, outside the graph). Programs whose kernels rewrite a packed
+ * weight's source, or a process with BL_NO_GRAPH set, launch one by one. */
 int bl_kernels_encode_range(bl_kernels *kernels, uint32_t first, uint32_t count,
                             uint32_t set);
 

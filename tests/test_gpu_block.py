@@ -81,3 +81,29 @@ def test_the_f16_block_is_within_its_tolerance(ctx, t, d, h):
     got = ir.run_on_gpu(ctx, g, block_values(ids, x, w), dtype=hip.F16)[ids.output]
     err = max_abs_err(got, want)
     assert err <= 2e-2, f"f16 block t={t} d={d}: max abs error {err:.3e}"
+
+
+def test_graph_replays_match_launches_one_by_one(ctx):
+    """encode_range replays a captured HIP graph of the block's kernels. Every
+    replay, with host writes, reads and one-by-one launches in between, must
+    equal the same kernels launched one by one on the same input, and the
+    oracle's block."""
+    t, d, h, mlp = 257, 384, 6, 1536
+    w = block_weights(d, mlp, 300, "xavier")
+    g, ids = block_graph(t, d, h, mlp, EPS)
+    prep = ir.prepare(ctx, g)
+    for tid, v in block_values(ids, oracle.normal(7, t * d), w).items():
+        prep.write(tid, v)
+    n = len(prep.kernels)
+    for rep in range(4):
+        x = oracle.normal(100 + rep, t * d)
+        prep.write(0, x)
+        for k in range(n):
+            prep.kernels.encode(k)
+        ctx.synchronize()
+        one_by_one = prep.read(ids.output)
+        prep.run()
+        ctx.synchronize()
+        replayed = prep.read(ids.output)
+        assert np.array_equal(replayed, one_by_one), f"replay {rep} differs from one-by-one launches"
+        assert_close(replayed, oracle.vit_block(x, w, t, h, d // h, mlp, EPS), f"replay {rep}")
