@@ -2,6 +2,8 @@
 // softmax, the tiled products with gathered operands (unfused attention
 // scores and values, the patch embedding), one-element-per-invocation kernels
 // (standalone map, class-token prepend, token drop) and a fixed-time spin.
+#include <cstdlib>
+
 #include "device_common.hpp"
 
 namespace bl {
@@ -69,6 +71,70 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LayerNormArgs a) {
     }
 }
 
+// Rows of 3 * LPR 16-byte chunks (384 f32 or f16 channels and the like):
+// LPR lanes per row, three chunks per lane, 64 / LPR rows per wave, so every
+// lane loads and every reduction stays inside its row's lanes. The row is
+// read once into registers. With NT (input and output larger than the
+// 256 MB Infinity Cache) the loads and stores are streaming (non-temporal);
+// otherwise they stay cached for the next kernel, which reads the output.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+template <typename T, int LPR, bool NT>
+__global__ __launch_bounds__(256) void layernorm3_kernel(LayerNormArgs a) {
+    constexpr int VEC = 16 / sizeof(T), RPW = 64 / LPR;
+    using V = typename std::conditional<sizeof(T) == 4, f32x4, f16x8>::type;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / LPR, l = lane % LPR;
+    const uint32_t row = a.row0 + (blockIdx.x * 4 + wave) * RPW + sub;
+    const bool ok = row < a.row1;
+    const uint32_t C = a.channels;
+    const T *x = (const T *)a.x + (uint64_t)(ok ? row : a.row0) * C;
+    float v[3][VEC];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const V *src = (const V *)(x + (l + LPR * i) * VEC);
+        const V chunk = NT ? __builtin_nontemporal_load(src) : *src;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            v[i][e] = to_f32(chunk[e]);
+            sum += v[i][e];
+        }
+    }
+    const float mean = row_sum<LPR>(sum) / (float)C;
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            const float d = v[i][e] - mean;
+            sq += d * d;
+        }
+    const float inv = 1.0f / sqrtf(row_sum<LPR>(sq) / (float)C + a.eps);
+    if (!ok) return;
+    const T *gamma = (const T *)a.gamma, *beta = (const T *)a.beta;
+    T *y = (T *)a.y + (uint64_t)row * C;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const uint32_t c = l + LPR * i;
+        const V gv = *(const V *)(gamma + c * VEC), bv = *(const V *)(beta + c * VEC);
+        V out;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            float r = (v[i][e] - mean) * inv * to_f32(gv[e]) + to_f32(bv[e]);
+            if (a.epi.n) r = apply_epilogue<T>(a.epi, r, (uint64_t)row * C + c * VEC + e);
+            out[e] = from_f32<T>(r);
+        }
+        if constexpr (NT) __builtin_nontemporal_store(out, (V *)(y + c * VEC));
+        else *(V *)(y + c * VEC) = out;
+    }
+}
+
 // Any width: three passes over the row in memory, one wave per row.
 template <typename T>
 __global__ __launch_bounds__(256) void layernorm_any_kernel(LayerNormArgs a) {
@@ -100,6 +166,21 @@ hipError_t ln_launch(const LayerNormArgs &a, hipStream_t s) {
     constexpr uint32_t VEC = 16 / sizeof(T);
     dim3 grid((a.row1 - a.row0 + 3) / 4), block(256);
     const uint32_t nch = a.channels / VEC;
+    if (a.channels % VEC == 0 && nch % 3 == 0 && !getenv("BL_LN_WAVE_ROW")) {
+        const uint32_t lpr = nch / 3, rows = a.row1 - a.row0;
+        auto grid3 = [&](uint32_t rpw) { return dim3((rows + 4 * rpw - 1) / (4 * rpw)); };
+        const bool nt = 2ull * rows * a.channels * sizeof(T) > (256ull << 20);
+#define BL_LN3(L, RPW)                                                                                 \
+    if (lpr == L) {                                                                                    \
+        if (nt) hipLaunchKernelGGL((layernorm3_kernel<T, L, true>), grid3(RPW), block, 0, s, a);       \
+        else hipLaunchKernelGGL((layernorm3_kernel<T, L, false>), grid3(RPW), block, 0, s, a);        \
+        return hipGetLastError();                                                                      \
+    }
+        BL_LN3(16, 4)
+        BL_LN3(32, 2)
+        BL_LN3(64, 1)
+#undef BL_LN3
+    }
     if (a.channels % VEC == 0) {
         if (nch <= 64) { hipLaunchKernelGGL((layernorm_kernel<T, 1>), grid, block, 0, s, a); return hipGetLastError(); }
         if (nch <= 128) { hipLaunchKernelGGL((layernorm_kernel<T, 2>), grid, block, 0, s, a); return hipGetLastError(); }
