@@ -679,15 +679,28 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
                 // waits better than a second round or idle CUs would.
                 const uint64_t w64 = wgs_of(TILE_64x64);
                 int chosen = (w64 >= ctx->compute_units && w64 <= 2ull * ctx->compute_units) ? TILE_64x64 : TILE_32x64;
+                ga.kgroups = 1;
+                ga.stages = 4;
+                // A long k with too few 64 x 64 tiles to go round (fc2 at the
+                // encoder's sizes: 132 tiles, 48 k-steps): 64 x 64 tiles with
+                // four groups of waves splitting k, two-stage rings each.
+                if (w64 <= ctx->compute_units && gk / 32 >= 32) {
+                    chosen = TILE_64x64;
+                    ga.kgroups = 4;
+                    ga.stages = 2;
+                }
                 if (const char *force = getenv("BL_GEMM_TILE")) {
                     int t = atoi(force);
                     if (t >= 0 && t < TILE_COUNT) chosen = t;
                 }
+                if (const char *force = getenv("BL_GEMM_KGROUPS")) ga.kgroups = (uint32_t)atoi(force);
+                if (const char *force = getenv("BL_GEMM_STAGES")) ga.stages = (uint32_t)atoi(force);
                 L.gemm = ga;
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
                           " " + std::to_string(gemm_tile_rows(chosen)) + "x" +
-                          std::to_string(gemm_tile_cols(chosen));
+                          std::to_string(gemm_tile_cols(chosen)) +
+                          (ga.kgroups > 1 ? " k" + std::to_string(ga.kgroups) : std::string());
                 break;
             }
             case BL_MAIN_ATTENTION_SCORES:

@@ -46,6 +46,8 @@ struct GemmArgs {
     int load;             // A: 0 rows of whole vectors, 1 element by element, 2 patches of an image
     int epi_mode;         // 0 none, 1 gelu_erf, 2 channel_scale(over n) + add, 3 any steps
     int pipeline;         // 1: the LDS-ring kernel with direct loads (k a multiple of 32)
+    uint32_t kgroups;     // pipelined kernel: groups of 4 waves splitting the k-steps (1, 2 or 4)
+    uint32_t stages;      // pipelined kernel: ring depth per group (2 .. 4)
     uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width
     EpilogueArgs epi;
     // The QKV projection of a flash attention kernel also writes that
