@@ -17,11 +17,11 @@
 //     order 0-3, 8-11, 4-7, 12-15 (bits 2 and 3 of the key swapped), which is
 //     the order in which that kernel's probabilities come out of its score
 //     accumulators.
-//  2. attn_kernel (f16 and bf16x3 math): the (head, 4 x QB x 32 query rows,
+//  2. attn_kernel (f16 and bf16x3 math): the (head, NW x 32 query rows,
 //     64-key tile) units are dealt out in equal contiguous runs to a fixed
-//     grid of workgroups (two per CU), so every CU gets the same amount of
+//     grid of workgroups (one per CU), so every CU gets the same amount of
 //     work whatever T and H are. A workgroup walks its run as segments of one
-//     (head, query tile) each; its 4 waves own QB blocks of 32 queries and
+//     (head, query tile) each; its NW = 8 waves own 32 queries each and
 //     share the K and Vt tiles, which stream through an LDS ring filled by
 //     direct 16-byte loads. Each wave computes the transposed scores
 //     S^T = K Q^T with v_mfma_f32_32x32x16, so a lane's accumulators hold 16
@@ -32,7 +32,7 @@
 //     most tiles skip the rescale of O; probabilities stay <= 2^8.
 //     A segment that covers all keys of its query tile writes the output; one
 //     that covers part of them writes (max, sum, unnormalised output) to
-//     scratch, and flash_merge_kernel combines them.
+//     scratch, and attn_merge_kernel combines them.
 //  3. flash16_kernel (f32 math, v_mfma_f32_16x16x4_f32): a workgroup owns 64
 //     queries of one head and one range of key tiles (split when there are
 //     too few query tiles to fill the chip); merged by flash16_merge_kernel.
