@@ -814,6 +814,18 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
         // One workgroup per CU (its 8 waves are two per SIMD).
         const uint64_t slots = std::max<uint32_t>(compute_units, 1);
         p.wgs = (uint32_t)std::min<uint64_t>(p.units, slots);
+        // Few units per CU (T in the low thousands): a run that crosses from
+        // one (head, query tile) to the next pays a second prologue and sets
+        // the kernel's tail. With a multiple of the pairs as the grid every
+        // run lies inside one pair: S runs per pair, the fewest that keep
+        // the longest run as short as floor(CUs / pairs) runs would.
+        const uint64_t pairs = (uint64_t)heads * p.qtiles;
+        if (pairs && pairs * 2 <= slots) {
+            const uint32_t s0 = (uint32_t)(slots / pairs);
+            const uint32_t longest = (kt + s0 - 1) / s0;
+            const uint32_t s = (kt + longest - 1) / longest;
+            p.wgs = (uint32_t)(pairs * s);
+        }
         if (const char *force = getenv("BL_FLASH_RUNS")) {
             const long w = atol(force);
             if (w > 0) p.wgs = (uint32_t)std::min<uint64_t>(p.units, (uint64_t)w);
