@@ -463,9 +463,88 @@ struct bl_kernels {
     bool graphs_ok = true;
 };
 
+namespace {
+
+// Activations stored as hi and lo bf16 planes (bf16x3 math): tensors the host
+// named internal, written by a LayerNorm, a GEMM or a flash attention kernel,
+// and read by nothing but the pipelined GEMM as its A operand. Each producer
+// launch gets the plane distance of its output, each reader of its A.
+void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, const uint32_t *internal,
+                            uint32_t n_internal) {
+    struct Use {
+        std::vector<uint32_t> producers, readers;
+        bool other = false;
+    };
+    std::vector<uint32_t> ids(internal, internal + n_internal);
+    std::sort(ids.begin(), ids.end());
+    auto is_internal = [&](uint32_t t) { return std::binary_search(ids.begin(), ids.end(), t); };
+    std::vector<std::pair<uint32_t, Use>> uses;
+    auto use_of = [&](uint32_t t) -> Use & {
+        for (auto &u : uses)
+            if (u.first == t) return u.second;
+        uses.push_back({t, Use{}});
+        return uses.back().second;
+    };
+    for (uint32_t ki = 0; ki < n; ki++) {
+        const bl_spec &s = specs[ki];
+        const uint32_t last = s.n_bindings - 1;
+        const uint32_t out_t = s.bindings[last].tensor;
+        for (uint32_t b = 0; b < last; b++) {
+            const uint32_t t = s.bindings[b].tensor;
+            if (!is_internal(t)) continue;
+            Use &u = use_of(t);
+            bool ok = s.main == BL_MAIN_MATMUL && b == s.reads[0] && t != out_t;
+            for (uint32_t c = 0; c < last && ok; c++)
+                if (c != b && s.bindings[c].tensor == t) ok = false;  // also an epilogue operand or B
+            for (uint32_t si = 0; si < ks->sets && ok; si++) {
+                const Launch &L = ks->kernels[ki].per_set[si];
+                ok = L.family == Family::GEMM && L.math == Math::SPLIT && L.gemm.load == 0 && L.gemm.pipeline &&
+                     L.gemm.k % 32 == 0;
+            }
+            if (ok) u.readers.push_back(ki);
+            else u.other = true;
+        }
+        if (!is_internal(out_t)) continue;
+        Use &u = use_of(out_t);
+        bool ok = true;
+        for (uint32_t si = 0; si < ks->sets && ok; si++) {
+            const Launch &L = ks->kernels[ki].per_set[si];
+            ok = L.math == Math::SPLIT && !L.f16 &&
+                 (L.family == Family::LAYER_NORM || L.family == Family::FLASH ||
+                  (L.family == Family::GEMM && L.gemm.load != 2 && !L.gemm.flash_ops));
+        }
+        if (ok) u.producers.push_back(ki);
+        else u.other = true;
+    }
+    for (auto &[t, u] : uses) {
+        if (u.other || u.producers.empty() || u.readers.empty()) continue;
+        for (uint32_t ki : u.producers) {
+            ks->kernels[ki].label += " > split";
+            for (Launch &L : ks->kernels[ki].per_set) {
+                if (L.family == Family::LAYER_NORM) L.ln.y_planes = (uint64_t)L.ln.rows * L.ln.channels;
+                else if (L.family == Family::GEMM) L.gemm.c_planes = (uint64_t)L.gemm.m * L.gemm.n;
+                else L.fl.out_planes = (uint64_t)L.fl.tokens * L.fl.heads * FLASH_HEAD_DIM;
+            }
+        }
+        for (uint32_t ki : u.readers) {
+            ks->kernels[ki].label += " < split";
+            for (Launch &L : ks->kernels[ki].per_set) L.gemm.a_planes = (uint64_t)L.gemm.m * L.gemm.k;
+        }
+    }
+}
+
+}  // namespace
+
 extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs, uint32_t n,
                                  const bl_binding_set *sets, uint32_t n_sets, bl_kernels **out) {
-    if (!ctx || !arenas || !out || (n && !specs) || (n_sets && !sets)) return BL_ERR_INVALID_ARGUMENT;
+    return bl_kernels_create_internal(ctx, arenas, specs, n, sets, n_sets, nullptr, 0, out);
+}
+
+extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs, uint32_t n,
+                                          const bl_binding_set *sets, uint32_t n_sets, const uint32_t *internal,
+                                          uint32_t n_internal, bl_kernels **out) {
+    if (!ctx || !arenas || !out || (n && !specs) || (n_sets && !sets) || (n_internal && !internal))
+        return BL_ERR_INVALID_ARGUMENT;
     *out = nullptr;
     hipSetDevice(ctx->device);
     const bl_binding_set identity{nullptr, 0};
@@ -832,6 +911,7 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
             }
         }
     }
+    if (n_internal && !getenv("BL_NO_SPLIT_ACTIVATIONS")) keep_split_activations(ks, specs, n, internal, n_internal);
     if (getenv("BL_NO_GRAPH")) ks->graphs_ok = false;
     bl_ctx_retain(ctx);
     *out = ks;

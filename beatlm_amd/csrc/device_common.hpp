@@ -122,6 +122,43 @@ __device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
 }
 
 
+// ---- f32 activations kept as hi and lo bf16 planes ----
+//
+// An activation the host never reads and that bf16x3 GEMMs read only as their
+// A operand is stored split, as the GEMM would split it: element i's hi part
+// at ((__bf16 *)base)[i] and its lo part `planes` elements further on
+// (planes = the tensor's element count, so the two planes fill the f32
+// tensor's bytes). planes == 0: plain f32 (or f16) storage.
+template <typename T>
+__device__ __forceinline__ void store_elem(T *base, uint64_t i, float v, uint64_t planes) {
+    if constexpr (sizeof(T) == 4) {
+        if (planes) {
+            __bf16 h, l;
+            split_bf16(v, h, l);
+            ((__bf16 *)base)[i] = h;
+            ((__bf16 *)base)[planes + i] = l;
+            return;
+        }
+    }
+    base[i] = from_f32<T>(v);
+}
+__device__ __forceinline__ void store_f32x4(float *base, uint64_t i, f32x4 v, uint64_t planes) {
+    if (planes) {
+        bf16x4 h, l;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            __bf16 hh, ll;
+            split_bf16(v[e], hh, ll);
+            h[e] = hh;
+            l[e] = ll;
+        }
+        *(bf16x4 *)((__bf16 *)base + i) = h;
+        *(bf16x4 *)((__bf16 *)base + planes + i) = l;
+    } else {
+        *(f32x4 *)(base + i) = v;
+    }
+}
+
 // ---- direct HBM/L2 -> LDS staging (global_load_lds_dwordx4) ----
 
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt in [3:0] and
@@ -149,6 +186,10 @@ __device__ __forceinline__ int swz(int row, int chunk) {
 // spread over the NWAVES waves of the workgroup in lane order. The lane's byte offsets from the
 // operand's tile base (its row, clamped to `row_limit`, and its swizzled
 // chunk) are computed once; a stage then costs one address add per load.
+//
+// With `halves` set (the bytes from one plane to another), a staged row is
+// two planes side by side: its chunks 0 .. CPR/2-1 come from the first plane
+// and CPR/2 .. CPR-1 from the same row of the second.
 template <int ROWS, int CPR, int NWAVES = 4>
 struct RowLoader {
     static constexpr int TOTAL = ROWS * CPR;
@@ -159,14 +200,17 @@ struct RowLoader {
     bool active[INSTR];
     int wave;
 
-    __device__ __forceinline__ RowLoader(uint32_t row_stride_bytes, uint32_t row_limit, int wave_, int lane) : wave(wave_) {
+    __device__ __forceinline__ RowLoader(uint32_t row_stride_bytes, uint32_t row_limit, int wave_, int lane,
+                                         uint32_t halves = 0)
+        : wave(wave_) {
 #pragma unroll
         for (int q = 0; q < INSTR; q++) {
             const int li = q * 64 + lane;
             const int i = wave * PER_WAVE + li;
             const int row = i / CPR, slot = i % CPR;
             const uint32_t r = min((uint32_t)row, row_limit);
-            off[q] = r * row_stride_bytes + swz<CPR>(row, slot) * 16;
+            const int c = swz<CPR>(row, slot);
+            off[q] = r * row_stride_bytes + (halves ? (c % (CPR / 2)) * 16 + (c / (CPR / 2)) * halves : c * 16);
             active[q] = li < PER_WAVE;
         }
     }

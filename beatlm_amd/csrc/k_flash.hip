@@ -500,7 +500,9 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
                     for (int j = 0; j < 4; j++) {
                         const int d = 32 * db + 8 * j + 4 * h;
                         if constexpr (SPLIT) {
-                            *(f32x4 *)(out + d) = f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]} * inv;
+                            store_f32x4((float *)args.out, ((uint64_t)q * H + head) * HD + d,
+                                        f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]} * inv,
+                                        args.out_planes);
                         } else {
                             f16x4 w;
 #pragma unroll
@@ -566,7 +568,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
     const float inv = 1.0f / l;
     T *out = (T *)a.out + ((uint64_t)q * H + head) * HD + d;
     if constexpr (M == Math::SPLIT) {
-        *(f32x4 *)out = acc * inv;
+        store_f32x4((float *)a.out, ((uint64_t)q * H + head) * HD + d, acc * inv, a.out_planes);
     } else {
         f16x4 w;
 #pragma unroll

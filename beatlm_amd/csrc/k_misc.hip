@@ -67,6 +67,12 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LayerNormArgs a) {
             if (a.epi.n) r = apply_epilogue<T>(a.epi, r, (uint64_t)row * C + c * VEC + e);
             out[e] = from_f32<T>(r);
         }
+        if constexpr (sizeof(T) == 4) {
+            if (a.y_planes) {
+                store_f32x4((float *)a.y, (uint64_t)row * C + c * VEC, out, a.y_planes);
+                continue;
+            }
+        }
         *(V *)(y + c * VEC) = out;
     }
 }
@@ -130,6 +136,12 @@ __global__ __launch_bounds__(256) void layernorm3_kernel(LayerNormArgs a) {
             if (a.epi.n) r = apply_epilogue<T>(a.epi, r, (uint64_t)row * C + c * VEC + e);
             out[e] = from_f32<T>(r);
         }
+        if constexpr (sizeof(T) == 4) {
+            if (a.y_planes) {
+                store_f32x4((float *)a.y, (uint64_t)row * C + c * VEC, out, a.y_planes);
+                continue;
+            }
+        }
         if constexpr (NT) __builtin_nontemporal_store(out, (V *)(y + c * VEC));
         else *(V *)(y + c * VEC) = out;
     }
@@ -153,11 +165,10 @@ __global__ __launch_bounds__(256) void layernorm_any_kernel(LayerNormArgs a) {
     }
     const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)C + a.eps);
     const T *gamma = (const T *)a.gamma, *beta = (const T *)a.beta;
-    T *y = (T *)a.y + (uint64_t)row * C;
     for (uint32_t c = lane; c < C; c += 64) {
         float r = (to_f32(x[c]) - mean) * inv * to_f32(gamma[c]) + to_f32(beta[c]);
         r = apply_epilogue<T>(a.epi, r, (uint64_t)row * C + c);
-        y[c] = from_f32<T>(r);
+        store_elem<T>((T *)a.y, (uint64_t)row * C + c, r, a.y_planes);
     }
 }
 

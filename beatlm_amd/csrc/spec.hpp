@@ -33,6 +33,7 @@ struct LayerNormArgs {
     uint32_t row0, row1;  // the part's rows
     float eps;
     EpilogueArgs epi;
+    uint64_t y_planes;    // y kept as hi and lo bf16 planes this many elements apart (0: as T)
 };
 
 struct GemmArgs {
@@ -56,6 +57,9 @@ struct GemmArgs {
     int flash_ops;
     void *fl_kp, *fl_vt;
     uint32_t fl_tpad;
+    // bf16x3 math: A, or C, kept as hi and lo bf16 planes this many elements
+    // apart (0: f32).
+    uint64_t a_planes, c_planes;
 };
 
 // B [k][n] -> the GEMM's packed operand (transposed, padded, converted).
@@ -104,6 +108,7 @@ struct FlashArgs {
     uint64_t units;
     uint32_t merge;       // 1 when some query tile's key tiles span two runs
     uint32_t prepped;     // 1 when the QKV projection already wrote K and Vt
+    uint64_t out_planes;  // bf16x3 math: out kept as hi and lo bf16 planes this many elements apart (0: f32)
 };
 
 // How a flash attention spec is launched: its grid and the scratch it needs

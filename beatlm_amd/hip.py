@@ -174,6 +174,11 @@ _SIGNATURES = {
         C.c_int,
         [_VP, _VP, C.POINTER(Spec), C.c_uint32, C.POINTER(BindingSet), C.c_uint32, C.POINTER(_VP)],
     ),
+    "bl_kernels_create_internal": (
+        C.c_int,
+        [_VP, _VP, C.POINTER(Spec), C.c_uint32, C.POINTER(BindingSet), C.c_uint32, C.POINTER(C.c_uint32), C.c_uint32,
+         C.POINTER(_VP)],
+    ),
     "bl_kernels_destroy": (None, [_VP]),
     "bl_kernels_len": (C.c_uint32, [_VP]),
     "bl_kernels_sets": (C.c_uint32, [_VP]),
@@ -300,7 +305,16 @@ class Arenas:
 class Kernels:
     """A program's kernels, checked and prepared once (bl_kernels)."""
 
-    def __init__(self, ctx: Context, arenas: Arenas, specs: list[Spec], sets: list[list[Substitution]] | None = None):
+    def __init__(
+        self,
+        ctx: Context,
+        arenas: Arenas,
+        specs: list[Spec],
+        sets: list[list[Substitution]] | None = None,
+        internal: list[int] | None = None,
+    ):
+        """`internal`: tensor ids the host never reads or writes (the program's
+        activations); the backend may keep them in a layout of its own."""
         self.ctx = ctx
         arr = (Spec * max(1, len(specs)))(*specs)
         sets = sets or []
@@ -313,8 +327,12 @@ class Kernels:
             set_arr[i].count = len(subs)
         self._keep = keep
         h = C.c_void_p()
+        internal = list(internal or [])
+        ids = (C.c_uint32 * max(1, len(internal)))(*internal)
         ctx.check(
-            ctx._lib.bl_kernels_create(ctx.handle, arenas.handle, arr, len(specs), set_arr, len(sets), C.byref(h))
+            ctx._lib.bl_kernels_create_internal(
+                ctx.handle, arenas.handle, arr, len(specs), set_arr, len(sets), ids, len(internal), C.byref(h)
+            )
         )
         self.handle = h
 

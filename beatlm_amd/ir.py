@@ -429,7 +429,9 @@ def realise(ctx: hip.Context, program: Program, dtype: int = hip.F32) -> Prepare
     program.set_dtype(dtype)
     plan = Plan(program.tensors(), profile("mi355x"))
     arenas = hip.Arenas(ctx, plan.arenas())
-    kernels = hip.Kernels(ctx, arenas, program.specs(plan))
+    # The host never touches activations: the backend may store them its own way.
+    activations = [t.id for t in program.tensors() if program.role(t.id) == ACTIVATION]
+    kernels = hip.Kernels(ctx, arenas, program.specs(plan), internal=activations)
     return Prepared(ctx, program, plan, arenas, kernels, dtype)
 
 

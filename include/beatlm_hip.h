@@ -226,6 +226,18 @@ int bl_arenas_device_ptr(bl_arenas *arenas, uint32_t arena, uint64_t offset,
 int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs,
                       uint32_t n_specs, const bl_binding_set *sets,
                       uint32_t n_sets, bl_kernels **out);
+/* bl_kernels_create, told which tensors (bl_binding.tensor ids) the host
+ * never reads or writes itself: the program's activations, which only its
+ * kernels produce and consume. The backend may keep those in a layout of its
+ * own; with bf16x3 f32 math, an activation every reader of which is a GEMM
+ * reading it as its A operand is stored as hi and lo bf16 planes, written
+ * split by its producer, so the GEMMs multiply it without splitting it.
+ * No counterpart in the reference (Kernels::new has no such hint); a host
+ * passes its plan's activation tensors, or calls bl_kernels_create. */
+int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs,
+                               uint32_t n_specs, const bl_binding_set *sets,
+                               uint32_t n_sets, const uint32_t *internal,
+                               uint32_t n_internal, bl_kernels **out);
 void bl_kernels_destroy(bl_kernels *kernels);
 uint32_t bl_kernels_len(const bl_kernels *kernels);
 uint32_t bl_kernels_sets(const bl_kernels *kernels);
