@@ -527,8 +527,21 @@ void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, co
             }
         }
         for (uint32_t ki : u.readers) {
-            ks->kernels[ki].label += " < split";
-            for (Launch &L : ks->kernels[ki].per_set) L.gemm.a_planes = (uint64_t)L.gemm.m * L.gemm.k;
+            Kernel &K = ks->kernels[ki];
+            K.label += " < split";
+            for (Launch &L : K.per_set) {
+                L.gemm.a_planes = (uint64_t)L.gemm.m * L.gemm.k;
+                // Without the split in its k-steps the plain 32 x 64 tile beats
+                // the long-k rule's 64 x 64 tile with four groups (fc2: 16.6
+                // against 18.8 us).
+                if (L.tile == TILE_64x64 && L.gemm.kgroups == 4 && !getenv("BL_GEMM_TILE") && !getenv("BL_GEMM_KGROUPS")) {
+                    L.tile = TILE_32x64;
+                    L.gemm.kgroups = 1;
+                    L.gemm.stages = 4;
+                    const size_t at = K.label.find(" 64x64 k4");
+                    if (at != std::string::npos) K.label.replace(at, 9, " 32x64");
+                }
+            }
         }
     }
 }
