@@ -249,6 +249,63 @@ class Graph:
         return ids
 
 
+class EncoderIds:
+    """The tensors of an encoder built by Graph.vit_encoder."""
+
+    def __init__(self, embed: EmbedIds, blocks: list, final_g: int, final_b: int, features: list, next_id: int):
+        self.embed = embed
+        self.blocks = blocks
+        self.final_g, self.final_b = final_g, final_b
+        self.features = features  # one [grid][grid][width] map per tapped layer, shallowest first
+        self.next_id = next_id
+
+
+def vit_encoder(
+    g: "Graph",
+    grid: int,
+    patch: int,
+    channels: int,
+    width: int,
+    heads: int,
+    mlp: int,
+    eps: float,
+    out_indices,
+    first_id: int = 0,
+    features_role: int = OUTPUT,
+) -> EncoderIds:
+    """The reference's encoder() (crates/beatlm/src/model/depth_anything_v2.rs
+    :434-527): patch embedding, class token and positions, the pre-LN blocks
+    up to the deepest tapped layer, and for each layer in `out_indices`
+    (1-based, as the checkpoint's config lists them) the shared final
+    LayerNorm of its hidden state and the token-to-map that drops the class
+    token, a [grid][grid][width] feature map of role `features_role`."""
+    tokens = grid * grid + 1
+    emb = g.vit_embeddings(grid, patch, channels, width, first_id)
+    x, nid = emb.output, emb.next_id
+    taps = set(out_indices)
+    blocks, taken = [], []
+    for layer in range(max(out_indices, default=0)):
+        ids = g.vit_block(VitDims(tokens, width, heads, mlp, eps), x, nid, ACTIVATION)
+        blocks.append(ids)
+        x, nid = ids.output, ids.next_id
+        if layer + 1 in taps:
+            taken.append(x)
+    final_g, final_b = nid, nid + 1
+    g.tensor(final_g, WEIGHT, width)
+    g.tensor(final_b, WEIGHT, width)
+    nid += 2
+    features = []
+    for hidden in taken:
+        normed, fmap = nid, nid + 1
+        g.tensor(normed, ACTIVATION, tokens * width)
+        g.push(op(OP_LAYER_NORM, [hidden, final_g, final_b], [tokens, width], eps), normed)
+        g.tensor(fmap, features_role, grid * grid * width)
+        g.push(op(OP_TOKENS_TO_MAP, [normed], [grid, grid, width]), fmap)
+        features.append(fmap)
+        nid += 2
+    return EncoderIds(emb, blocks, final_g, final_b, features, nid)
+
+
 def output_elements(o: Op) -> int:
     return int(_lib().bli_op_output_elements(C.byref(o)))
 

@@ -107,3 +107,46 @@ def test_graph_replays_match_launches_one_by_one(ctx):
         replayed = prep.read(ids.output)
         assert np.array_equal(replayed, one_by_one), f"replay {rep} differs from one-by-one launches"
         assert_close(replayed, oracle.vit_block(x, w, t, h, d // h, mlp, EPS), f"replay {rep}")
+
+
+@pytest.mark.parametrize("dtype,taps", [(hip.F32, [1, 2, 4]), (hip.F16, [1, 2])])
+def test_the_encoders_feature_maps_match_the_oracle(ctx, dtype, taps):
+    """encoder() (depth_anything_v2.rs:434-527) at 224 pixels: embeddings,
+    blocks up to the deepest tap, and per tap the shared final LayerNorm and
+    the token-to-map, against the oracle composed op by op."""
+    grid, patch, d, h, mlp = 16, 14, 384, 6, 1536
+    t = grid * grid + 1
+    g = ir.Graph()
+    enc = ir.vit_encoder(g, grid, patch, 3, d, h, mlp, EPS, taps)
+    image = oracle.uniform(60, (grid * patch) ** 2 * 3, 0.0, 1.0)
+    pw = oracle.fan_in_weights(61, patch * patch * 3 * d, patch * patch * 3)
+    pb = oracle.uniform(62, d, -0.1, 0.1)
+    cls = oracle.uniform(63, d, -1.0, 1.0)
+    pos = oracle.uniform(64, t * d, -0.5, 0.5)
+    fg, fb = oracle.uniform(65, d, 0.8, 1.2), oracle.uniform(66, d, -0.1, 0.1)
+    weights = [block_weights(d, mlp, 100 + 20 * i, "reference") for i in range(len(enc.blocks))]
+    vals = {enc.embed.image: image, enc.embed.patch_w: pw, enc.embed.patch_b: pb, enc.embed.cls: cls,
+            enc.embed.pos: pos, enc.final_g: fg, enc.final_b: fb}
+    for ids, w in zip(enc.blocks, weights):
+        for name in ir.BLOCK_WEIGHTS:
+            vals[getattr(ids, name)] = w[name]
+    if dtype == hip.F16:
+        vals = {k: v.astype(np.float16) for k, v in vals.items()}
+    f32 = {k: v.astype(np.float32) for k, v in vals.items()}
+    e = enc.embed
+    x = oracle.add(oracle.prepend_token(f32[e.cls], oracle.patch_embed(f32[e.image], f32[e.patch_w], f32[e.patch_b],
+                                                                          grid, grid, patch, 3, d), grid * grid, d),
+                   f32[e.pos])
+    want = []
+    for i, ids in enumerate(enc.blocks):
+        w = {name: f32[getattr(ids, name)] for name in ir.BLOCK_WEIGHTS}
+        x = oracle.vit_block(x, w, t, h, d // h, mlp, EPS)
+        if i + 1 in taps:
+            want.append(oracle.layernorm(x, f32[enc.final_g], f32[enc.final_b], t, d, EPS)[d:])
+    got = ir.run_on_gpu(ctx, g, vals, dtype=dtype)
+    for tap, fmap, w in zip(taps, enc.features, want):
+        case = f"feature map of layer {tap}, {'f16' if dtype == hip.F16 else 'f32'}"
+        if dtype == hip.F16:
+            assert max_abs_err(got[fmap], w) <= 2e-2, case
+        else:
+            assert_close(got[fmap], w, case)

@@ -161,6 +161,27 @@ def test_the_model_builder_lowers_to_the_same_kernels():
     assert emb.next_id == 8
 
 
+def test_the_encoder_taps_its_layers_through_the_final_norm_into_feature_maps():
+    """encoder() (depth_anything_v2.rs:434-527): embeddings, the blocks up to
+    the deepest tap, then per tap the shared final LayerNorm and the
+    token-to-map, whose outputs are the features."""
+    g = Graph()
+    enc = ir.vit_encoder(g, 16, 14, 3, D, HEADS, MLP, 1e-6, [1, 2, 4])
+    assert len(enc.blocks) == 4 and len(enc.features) == 3
+    p = g.lower()
+    names = p.names()
+    assert names[:2] == ["patch_embed", "prepend_token+add"]
+    assert names[-6:] == ["layernorm", "tokens_to_map"] * 3
+    assert len(names) == 2 + 4 * 9 + 6
+    assert all(p.role(f) == OUTPUT for f in enc.features)
+    # Each tapped hidden state feeds the next block and the final norm; its
+    # lifetime runs to the norm that reads it.
+    tapped = [enc.blocks[i].output for i in (0, 1, 3)]
+    assert all(p.role(t) == ACTIVATION for t in tapped)
+    assert p.lifetime(tapped[0])[1] >= 2 + 4 * 9
+    assert p.fuse_attention().names().count("flash_attention") == 4
+
+
 def shapes():
     """One kernel of each kind the block uses, at small ragged sizes."""
     yield "layernorm", [(X, INPUT, 41 * 7), (1, WEIGHT, 7), (2, WEIGHT, 7)], op(ir.OP_LAYER_NORM, [X, 1, 2], [41, 7], 1e-5)
