@@ -531,15 +531,16 @@ void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, co
             K.label += " < split";
             for (Launch &L : K.per_set) {
                 L.gemm.a_planes = (uint64_t)L.gemm.m * L.gemm.k;
-                // Without the split in its k-steps the plain 32 x 64 tile beats
-                // the long-k rule's 64 x 64 tile with four groups (fc2: 16.6
-                // against 18.8 us).
+                // Without the split in its k-steps the 32 x 64 tile with 64-wide
+                // steps in a 3-stage ring beats the long-k rule's 64 x 64 tile
+                // with four groups (fc2: 15.7 against 18.8 us).
                 if (L.tile == TILE_64x64 && L.gemm.kgroups == 4 && !getenv("BL_GEMM_TILE") && !getenv("BL_GEMM_KGROUPS")) {
                     L.tile = TILE_32x64;
                     L.gemm.kgroups = 1;
-                    L.gemm.stages = 4;
+                    L.gemm.stages = 3;
+                    L.gemm.kslices = L.gemm.k % 64 == 0 ? 2 : 1;
                     const size_t at = K.label.find(" 64x64 k4");
-                    if (at != std::string::npos) K.label.replace(at, 9, " 32x64");
+                    if (at != std::string::npos) K.label.replace(at, 9, L.gemm.kslices == 2 ? " 32x64 bk64" : " 32x64");
                 }
             }
         }
@@ -787,6 +788,8 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 }
                 if (const char *force = getenv("BL_GEMM_KGROUPS")) ga.kgroups = (uint32_t)atoi(force);
                 if (const char *force = getenv("BL_GEMM_STAGES")) ga.stages = (uint32_t)atoi(force);
+                ga.kslices = 1;
+                if (const char *force = getenv("BL_GEMM_KSLICES")) ga.kslices = (uint32_t)atoi(force);
                 L.gemm = ga;
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +

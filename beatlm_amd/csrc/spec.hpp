@@ -49,6 +49,7 @@ struct GemmArgs {
     int pipeline;         // 1: the LDS-ring kernel with direct loads (k a multiple of 32)
     uint32_t kgroups;     // pipelined kernel: groups of 4 waves splitting the k-steps (1, 2 or 4)
     uint32_t stages;      // pipelined kernel: ring depth per group (2 .. 4)
+    uint32_t kslices;     // pipelined kernel: 32-wide k-slices per ring stage (1 or 2)
     uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width
     EpilogueArgs epi;
     // The QKV projection of a flash attention kernel also writes that
