@@ -43,7 +43,9 @@ SOURCES = [
     "backend.cpp",
     "timer.cpp",
     "ir.cpp",
+    "cost.cpp",
     "schedule.cpp",
+    "step.cpp",
 ]
 
 

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "timer.hpp"
+#include "../../include/beatlm_schedule.h"
 
 namespace {
 
@@ -51,7 +52,7 @@ struct bl_timer {
 };
 
 // The most slices one frame can time.
-static constexpr uint32_t TIMER_MAX_SLICES = 4096;
+static constexpr uint32_t TIMER_MAX_SLICES = BLS_TIMER_MAX_SLICES;  // what timer_capacity checks against
 
 extern "C" int bl_timer_create(bl_ctx *ctx, uint32_t max_slices, bl_timer **out) {
     if (!ctx || !out) return BL_ERR_INVALID_ARGUMENT;

@@ -161,7 +161,7 @@ def test_fixed_latency_delivers_exactly_on_its_frame():
     s = S.Scheduler(2, S.MISS_DROP, 1000)
     c = cost()
     job = s.submit(frame(10), [0], c)
-    assert s.due(job) == 12
+    assert s.due(job) == S.Due.frame(12)
     p10 = s.plan_frame(frame(10), 1000, c)
     assert len(p10.runs) == 1 and not p10.delivered and not p10.missed
     p11 = s.plan_frame(frame(11), 1000, c)
@@ -180,7 +180,7 @@ def test_a_lone_job_that_cannot_finish_runs_to_its_deadline_and_is_missed_there(
         assert len(p.runs) == 1 and not p.delivered and not p.missed, f
     p = s.plan_frame(frame(2), 100, c)
     assert len(p.runs) == 1 and p.runs[0].position == 2 and not p.delivered
-    assert p.missed == [S.Missed(job, 0, 2, S.MISS_HOLD_PREVIOUS)]
+    assert p.missed == [S.Missed(job, 0, S.Due.frame(2), S.MISS_HOLD_PREVIOUS)]
     assert s.pending() == 0
     for f in range(3, 6):
         later = s.plan_frame(frame(f), 100, c)
@@ -198,7 +198,7 @@ def test_a_forecast_above_the_real_budget_delays_the_miss_to_its_deadline():
         assert not p.delivered and not p.missed
     p = s.plan_frame(frame(2), 100, c)
     assert ran == 2 and len(p.runs) == 1 and not p.delivered
-    assert [(m.job, m.due) for m in p.missed] == [(job, 2)]
+    assert [(m.job, m.due) for m in p.missed] == [(job, S.Due.frame(2))]
 
 
 def test_a_dip_in_one_frame_does_not_abandon_a_job_the_later_frames_finish():
@@ -222,7 +222,7 @@ def test_an_abandoned_job_frees_the_job_behind_it():
     b = s.submit(frame(0), [3], c)
     p0 = s.plan_frame(frame(0), 100, c)
     assert [r.job for r in p0.runs] == [b]
-    assert p0.missed == [S.Missed(a, 0, 1, S.MISS_DROP)]
+    assert p0.missed == [S.Missed(a, 0, S.Due.frame(1), S.MISS_DROP)]
     p1 = s.plan_frame(frame(1), 100, c)
     assert [d.job for d in p1.delivered] == [b]
     for f in range(2, 5):
@@ -239,7 +239,7 @@ def test_a_late_lone_job_is_abandoned_once_a_job_queues_behind_it():
     b = s.submit(frame(1), [4], c)
     p1 = s.plan_frame(frame(1), 100, c)
     assert [(r.job, r.position) for r in p1.runs] == [(b, 0)]
-    assert p1.missed == [S.Missed(a, 0, 2, S.MISS_DROP)]
+    assert p1.missed == [S.Missed(a, 0, S.Due.frame(2), S.MISS_DROP)]
     delivered = []
     for f in range(2, 6):
         p = s.plan_frame(frame(f), 100, c)
@@ -257,7 +257,7 @@ def test_a_job_whose_deadline_has_passed_is_not_waiting_behind_a_late_one():
     assert [r.job for r in p3.runs] == [a]
     assert [m.job for m in p3.missed] == [b]
     p4 = s.plan_frame(frame(4), 100, c)
-    assert len(p4.runs) == 1 and [(m.job, m.due) for m in p4.missed] == [(a, 4)] and not p4.delivered
+    assert len(p4.runs) == 1 and [(m.job, m.due) for m in p4.missed] == [(a, S.Due.frame(4))] and not p4.delivered
 
 
 def test_miss_policy_is_carried_through():
