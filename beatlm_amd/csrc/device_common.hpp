@@ -43,6 +43,14 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The sum over the LPR consecutive lanes that hold one row (LPR a power of 2).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
 // ---- the attention's value operand layout ----
 // Position of key k inside a row of the transposed values Vt for the 32 x 32
 // flash kernel: bits 2 and 3 of k swapped, so each 16-key group is stored in

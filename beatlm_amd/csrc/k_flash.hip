@@ -279,33 +279,47 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
             asm volatile("" ::: "memory");
         };
 
-        // The wave's 32 queries, pre-scaled by scale * log2(e), as the B operand
-        // of S^T = K Q^T: lane (l32, h) holds d = 16 ds + 8 h + e of query q.
-        V8 qh[4], ql[4];
+        // The wave's 32 queries as they are stored: lane (l32, h) loads d =
+        // 16 ds + 8 h + e of query q. Issued before the segment's first K and Vt
+        // tiles, so one wait covers both.
+        f32x4 qa[4], qb[4];
+        f16x8 q16[4];
         {
             const bool ok = q < args.row1;
             const T *qrow = (const T *)args.qkv + (uint64_t)q * row_stride + head * HD + 8 * h;
 #pragma unroll
             for (int ds = 0; ds < 4; ds++) {
                 if constexpr (SPLIT) {
-                    f32x4 a = {}, b = {};
+                    qa[ds] = f32x4{0, 0, 0, 0};
+                    qb[ds] = f32x4{0, 0, 0, 0};
                     if (ok) {
-                        a = *(const f32x4 *)(qrow + 16 * ds);
-                        b = *(const f32x4 *)(qrow + 16 * ds + 4);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        __bf16 hi, lo;
-                        split_bf16((e < 4 ? a[e] : b[e - 4]) * c, hi, lo);
-                        qh[ds][e] = hi;
-                        ql[ds][e] = lo;
+                        qa[ds] = *(const f32x4 *)(qrow + 16 * ds);
+                        qb[ds] = *(const f32x4 *)(qrow + 16 * ds + 4);
                     }
                 } else {
-                    f16x8 a = {};
-                    if (ok) a = *(const f16x8 *)(qrow + 16 * ds);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) qh[ds][e] = (_Float16)((float)a[e] * c);
+                    q16[ds] = f16x8{};
+                    if (ok) q16[ds] = *(const f16x8 *)(qrow + 16 * ds);
                 }
+            }
+        }
+        for (uint32_t t = k0; t < k0 + STAGES - 1 && t < k1; t++) issue(t);
+        arrive(k0);
+        // The queries pre-scaled by scale * log2(e), as the B operand of
+        // S^T = K Q^T.
+        V8 qh[4], ql[4];
+#pragma unroll
+        for (int ds = 0; ds < 4; ds++) {
+            if constexpr (SPLIT) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    __bf16 hi, lo;
+                    split_bf16((e < 4 ? qa[ds][e] : qb[ds][e - 4]) * c, hi, lo);
+                    qh[ds][e] = hi;
+                    ql[ds][e] = lo;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) qh[ds][e] = (_Float16)((float)q16[ds][e] * c);
             }
         }
 
@@ -476,8 +490,6 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
             asm volatile("" ::: "memory");
         };
 
-        for (uint32_t t = k0; t < k0 + STAGES - 1 && t < k1; t++) issue(t);
-        arrive(k0);
         f32x16 sa[2], sb[2];
         scores(k0, bq, sa);
         uint32_t t = k0;
@@ -534,8 +546,11 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
 // Combines the partial results of the query tiles whose key tiles were spread
 // over more than one run: O = sum_r 2^(m_r - m) O_r / sum_r 2^(m_r - m) l_r,
 // folded run by run with a running max. A workgroup takes 16 rows of one
-// (head, query tile); one invocation per (row, 4 columns).
+// (head, query tile); one invocation per (row, 4 columns). The runs are taken
+// MERGE_BATCH at a time, every load of a batch issued before the first is
+// used, so a row pays one memory round trip per batch instead of one per run.
 constexpr uint32_t MERGE_ROWS = 16;
+constexpr uint32_t MERGE_BATCH = 8;
 template <Math M>
 __global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
     using T = typename FlashTraits<M>::T;
@@ -555,14 +570,32 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
     const uint32_t first_slot = run_begin(vf, U, G) < u0 ? 1 : 0;
     float m = -INFINITY, l = 0.0f;
     f32x4 acc = {0, 0, 0, 0};
-    for (uint32_t v = vf; v <= vl; v++) {
-        const uint64_t row = ((uint64_t)v * 2 + (v == vf ? first_slot : 0)) * QROWS + r;
-        const f32x2 st = *(const f32x2 *)(a.stats + 2 * row);
-        const f32x4 ov = *(const f32x4 *)(a.partial + row * HD + d);
-        const float m_new = fmaxf(m, st[0]);
-        const float wa = __builtin_amdgcn_exp2f(m - m_new), wb = __builtin_amdgcn_exp2f(st[0] - m_new);
-        l = l * wa + st[1] * wb;
-        acc = acc * wa + ov * wb;
+    for (uint32_t v0 = vf; v0 <= vl; v0 += MERGE_BATCH) {
+        f32x2 st[MERGE_BATCH];
+        f32x4 ov[MERGE_BATCH];
+#pragma unroll
+        for (uint32_t b = 0; b < MERGE_BATCH; b++) {
+            const uint32_t v = v0 + b;
+            st[b] = f32x2{-INFINITY, 0.0f};
+            ov[b] = f32x4{0, 0, 0, 0};
+            if (v <= vl) {
+                const uint64_t row = ((uint64_t)v * 2 + (v == vf ? first_slot : 0)) * QROWS + r;
+                st[b] = *(const f32x2 *)(a.stats + 2 * row);
+                ov[b] = *(const f32x4 *)(a.partial + row * HD + d);
+            }
+        }
+        float m_new = m;
+#pragma unroll
+        for (uint32_t b = 0; b < MERGE_BATCH; b++) m_new = fmaxf(m_new, st[b][0]);
+        const float wa = __builtin_amdgcn_exp2f(m - m_new);
+        l *= wa;
+        acc *= wa;
+#pragma unroll
+        for (uint32_t b = 0; b < MERGE_BATCH; b++) {
+            const float wb = __builtin_amdgcn_exp2f(st[b][0] - m_new);  // 0 for a run past vl
+            l += st[b][1] * wb;
+            acc += ov[b] * wb;
+        }
         m = m_new;
     }
     const float inv = 1.0f / l;

@@ -83,13 +83,6 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LayerNormArgs a) {
 // read once into registers. With NT (input and output larger than the
 // 256 MB Infinity Cache) the loads and stores are streaming (non-temporal);
 // otherwise they stay cached for the next kernel, which reads the output.
-template <int LPR>
-__device__ __forceinline__ float row_sum(float v) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
-
 template <typename T, int LPR, bool NT>
 __global__ __launch_bounds__(256) void layernorm3_kernel(LayerNormArgs a) {
     constexpr int VEC = 16 / sizeof(T), RPW = 64 / LPR;
