@@ -280,7 +280,7 @@ extern "C" int bl_arenas_device_ptr(bl_arenas *a, uint32_t arena, uint64_t offse
 
 namespace {
 
-enum class Family { LAYER_NORM, GEMM, GATHER, SOFTMAX, FLASH, ELEMENT };
+enum class Family { LAYER_NORM, GEMM, GATHER, SOFTMAX, FLASH, ELEMENT, DPT };
 
 struct Launch {
     Family family;
@@ -296,6 +296,8 @@ struct Launch {
     SoftmaxArgs sm;
     FlashArgs fl;
     ElementArgs el;
+    Dpt dpt = Dpt::RESIZE;
+    DptArgs dp;
 };
 
 struct Kernel {
@@ -329,6 +331,9 @@ const char *main_name(uint32_t m) {
     case BL_MAIN_TOKENS_TO_MAP: return "tokens_to_map";
     case BL_MAIN_MAP: return "map";
     case BL_MAIN_FLASH_ATTENTION: return "flash_attention";
+    case BL_MAIN_CONV3X3: return "conv2d3x3";
+    case BL_MAIN_CONV_TRANSPOSE: return "conv_transpose2d";
+    case BL_MAIN_RESIZE_BILINEAR: return "resize_bilinear";
     default: return nullptr;
     }
 }
@@ -422,6 +427,30 @@ bool shape_of(const bl_spec &s, Shape &sh, std::string &why) {
         sh.out = d[0];
         sh.extent = d[0];
         return d[0] != 0;
+    case BL_MAIN_CONV3X3: {
+        if (!d[4]) { why = "a stride of zero"; return false; }
+        const uint64_t oh = (d[0] - 1) / d[4] + 1, ow = (d[1] - 1) / d[4] + 1;
+        sh.reads = {mul({d[0], d[1], d[2]}), mul({9, d[2], d[3]})};
+        if (d[5]) sh.reads.push_back(d[3]);
+        sh.out = mul({oh, ow, d[3]});
+        sh.extent = (uint32_t)std::min<uint64_t>(oh * ow, UINT32_MAX);
+        sh.grain = 64;
+        sh.per_unit = d[3];
+        return d[0] && d[1] && d[2] && d[3];
+    }
+    case BL_MAIN_CONV_TRANSPOSE:
+        sh.reads = {mul({d[0], d[1], d[2]}), mul({d[4], d[4], d[2], d[3]})};
+        if (d[5]) sh.reads.push_back(d[3]);
+        sh.out = mul({d[0], d[4], d[1], d[4], d[3]});
+        sh.extent = (uint32_t)std::min<uint64_t>(mul({d[0], d[4], d[1], d[4]}), UINT32_MAX);
+        sh.per_unit = d[3];
+        return d[0] && d[1] && d[2] && d[3] && d[4];
+    case BL_MAIN_RESIZE_BILINEAR:
+        sh.reads = {mul({d[0], d[1], d[4]})};
+        sh.out = mul({d[2], d[3], d[4]});
+        sh.extent = (uint32_t)std::min<uint64_t>(mul({d[2], d[3]}), UINT32_MAX);
+        sh.per_unit = d[4];
+        return d[0] && d[1] && d[2] && d[3] && d[4];
     case BL_MAIN_FLASH_ATTENTION:
         sh.reads = {mul({d[0], 3, d[1], d[2]})};
         sh.out = mul({d[0], d[1], d[2]});
@@ -639,6 +668,9 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
             return bad(BL_ERR_KERNEL, "kernel %s: part %u/%u covers %u..%u of %u (grain %u)", name.c_str(),
                        pt.index + 1, pt.count, pt.start, pt.end, sh.extent, sh.grain);
 
+        if (s.prologue && !(s.prologue == BL_PRO_RELU && s.main == BL_MAIN_CONV3X3))
+            return bad(BL_ERR_KERNEL, "kernel %s: prologue %u on a main operation that takes none", name.c_str(), s.prologue);
+        if (s.prologue == BL_PRO_RELU) name = "relu-" + name;
         Kernel k;
         k.label = name;
         if (pt.count > 1) k.label += " part " + std::to_string(pt.index + 1) + "/" + std::to_string(pt.count);
@@ -697,13 +729,15 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 variant = "wave-per-row";
                 break;
             case BL_MAIN_MATMUL:
-            case BL_MAIN_PATCH_EMBED: {
+            case BL_MAIN_PATCH_EMBED:
+            case BL_MAIN_CONV3X3: {
                 L.family = Family::GEMM;
-                const bool patch = s.main == BL_MAIN_PATCH_EMBED;
-                const uint32_t gm = patch ? d[0] * d[1] : d[0];
-                const uint32_t gk = patch ? d[2] * d[2] * d[3] : d[1];
-                const uint32_t gn = patch ? d[4] : d[2];
-                const bool has_bias = patch ? d[5] != 0 : d[3] != 0;
+                const bool patch = s.main == BL_MAIN_PATCH_EMBED, conv = s.main == BL_MAIN_CONV3X3;
+                const uint32_t conv_oh = conv ? (d[0] - 1) / d[4] + 1 : 0, conv_ow = conv ? (d[1] - 1) / d[4] + 1 : 0;
+                const uint32_t gm = patch ? d[0] * d[1] : conv ? conv_oh * conv_ow : d[0];
+                const uint32_t gk = patch ? d[2] * d[2] * d[3] : conv ? 9 * d[2] : d[1];
+                const uint32_t gn = patch ? d[4] : conv ? d[3] : d[2];
+                const bool has_bias = (patch || conv) ? d[5] != 0 : d[3] != 0;
                 GemmArgs ga{};
                 ga.a = rd(0);
                 ga.bias = has_bias ? rd(2) : nullptr;
@@ -715,13 +749,21 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 ga.n_pad = (gn + PACK_N - 1) / PACK_N * PACK_N;
                 ga.row0 = pt.start;
                 ga.row1 = pt.end;
-                ga.load = patch ? 2 : 0;
+                ga.load = patch ? 2 : conv ? 3 : 0;
                 ga.pipeline = getenv("BL_GEMM_NO_PIPELINE") ? 0 : 1;
                 if (patch) {
                     ga.p0 = d[1];
                     ga.p1 = d[2];
                     ga.p2 = d[3];
                     ga.p3 = d[1] * d[2];
+                }
+                if (conv) {
+                    ga.p0 = d[0];
+                    ga.p1 = d[1];
+                    ga.p2 = d[2];
+                    ga.p3 = d[4];
+                    ga.p4 = conv_ow;
+                    ga.p5 = s.prologue == BL_PRO_RELU ? 1 : 0;
                 }
                 ga.epi = epi;
                 // Epilogues with a kernel of their own: GELU (erf); LayerScale over the
@@ -833,6 +875,29 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 L.el = ElementArgs{rd(0), nullptr, out_ptr, pt.start, pt.end, 0, epi};
                 variant = "per-element";
                 break;
+            case BL_MAIN_CONV_TRANSPOSE:
+            case BL_MAIN_RESIZE_BILINEAR: {
+                L.family = Family::DPT;
+                const bool ct = s.main == BL_MAIN_CONV_TRANSPOSE;
+                L.dpt = ct ? Dpt::CONV_TRANSPOSE : Dpt::RESIZE;
+                L.dp = DptArgs{};
+                L.dp.x = rd(0);
+                L.dp.w = ct ? rd(1) : nullptr;
+                L.dp.bias = ct && d[5] ? rd(2) : nullptr;
+                L.dp.y = out_ptr;
+                for (int i = 0; i < 6; i++) L.dp.d[i] = d[i];
+                // ResizeBilinear::ratios (kernel.rs:614-631): (in - 1) / (out - 1)
+                // in f32, zero for one output row or column.
+                if (!ct) {
+                    L.dp.ry = d[2] > 1 ? (float)(d[0] - 1) / (float)(d[2] - 1) : 0.0f;
+                    L.dp.rx = d[3] > 1 ? (float)(d[1] - 1) / (float)(d[3] - 1) : 0.0f;
+                }
+                L.dp.start = (uint64_t)pt.start * sh.per_unit;
+                L.dp.end = (uint64_t)pt.end * sh.per_unit;
+                L.dp.epi = epi;
+                variant = "per-element";
+                break;
+            }
             case BL_MAIN_FLASH_ATTENTION: {
                 if (s.n_epilogue) return bad(BL_ERR_KERNEL, "kernel %s: the flash kernel takes no epilogue", name.c_str());
                 L.family = Family::FLASH;
@@ -970,6 +1035,7 @@ static hipError_t launch(const Launch &L, hipStream_t s) {
     case Family::SOFTMAX: return launch_softmax(L.sm, L.f16, s);
     case Family::FLASH: return launch_flash(L.fl, L.math, s);
     case Family::ELEMENT: return launch_element(L.el, L.element, L.f16, s);
+    case Family::DPT: return launch_dpt(L.dp, L.dpt, L.f16, s);
     }
     return hipErrorInvalidValue;
 }

@@ -83,10 +83,27 @@ std::vector<std::pair<uint32_t, uint64_t>> op_reads(const bli_op &o) {
     case BLI_OP_GELU_ERF:
     case BLI_OP_SCALE: r = {{t[0], d[0]}}; break;
     case BLI_OP_CHANNEL_SCALE: r = {{t[0], product({d[0], d[1]})}, {t[1], d[1]}}; break;
+    case BLI_OP_CONV3X3:
+        r = {{t[0], product({d[0], d[1], d[2]})}, {t[1], product({9, d[2], d[3]})}};
+        if (t[2] != BLI_NONE) r.push_back({t[2], d[3]});
+        break;
+    case BLI_OP_CONV1X1:
+        r = {{t[0], product({d[0], d[1], d[2]})}, {t[1], product({d[2], d[3]})}};
+        if (t[2] != BLI_NONE) r.push_back({t[2], d[3]});
+        break;
+    case BLI_OP_CONV_TRANSPOSE:
+        r = {{t[0], product({d[0], d[1], d[2]})}, {t[1], product({d[4], d[4], d[2], d[3]})}};
+        if (t[2] != BLI_NONE) r.push_back({t[2], d[3]});
+        break;
+    case BLI_OP_RESIZE_BILINEAR: r = {{t[0], product({d[0], d[1], d[4]})}}; break;
     default: break;
     }
     return r;
 }
+
+// Conv2d3x3::out_height / strided (kernel.rs:479-507): a 3x3 window with
+// padding 1 at `stride`, (extent - 1) / stride + 1.
+uint32_t strided(uint32_t extent, uint32_t stride) { return (extent == 0 || stride == 0) ? 0 : (extent - 1) / stride + 1; }
 
 // OpKind::output_elements (kernel.rs:977-1005).
 uint64_t op_output(const bli_op &o) {
@@ -106,6 +123,10 @@ uint64_t op_output(const bli_op &o) {
     case BLI_OP_GELU_ERF:
     case BLI_OP_SCALE: return d[0];
     case BLI_OP_CHANNEL_SCALE: return product({d[0], d[1]});
+    case BLI_OP_CONV3X3: return product({strided(d[0], d[4]), strided(d[1], d[4]), d[3]});
+    case BLI_OP_CONV1X1: return product({d[0], d[1], d[3]});
+    case BLI_OP_CONV_TRANSPOSE: return product({d[0], d[4], d[1], d[4], d[3]});
+    case BLI_OP_RESIZE_BILINEAR: return product({d[2], d[3], d[4]});
     default: return 0;
     }
 }
@@ -121,7 +142,8 @@ bool op_has_zero_dim(const bli_op &o) {
     switch (o.kind) {
     case BLI_OP_LAYER_NORM: case BLI_OP_SOFTMAX: case BLI_OP_PREPEND_TOKEN: case BLI_OP_CHANNEL_SCALE: return any0(2);
     case BLI_OP_MATMUL: case BLI_OP_ATTENTION_SCORES: case BLI_OP_ATTENTION_VALUES: case BLI_OP_TOKENS_TO_MAP: return any0(3);
-    case BLI_OP_PATCH_EMBED: return any0(5);
+    case BLI_OP_PATCH_EMBED: case BLI_OP_CONV3X3: case BLI_OP_CONV_TRANSPOSE: case BLI_OP_RESIZE_BILINEAR: return any0(5);
+    case BLI_OP_CONV1X1: return any0(4);
     default: return any0(1);
     }
 }
@@ -150,11 +172,17 @@ struct MainOp {
         case BL_MAIN_ATTENTION_SCORES: return product({d[0], d[1], d[0]});
         case BL_MAIN_ATTENTION_VALUES: case BL_MAIN_FLASH_ATTENTION: return product({d[0], d[1], d[2]});
         case BL_MAIN_MAP: return d[0];
+        case BL_MAIN_CONV3X3: return product({strided(d[0], d[4]), strided(d[1], d[4]), d[3]});
+        case BL_MAIN_CONV_TRANSPOSE: return product({d[0], d[4], d[1], d[4], d[3]});
+        case BL_MAIN_RESIZE_BILINEAR: return product({d[2], d[3], d[4]});
         default: return 0;
         }
     }
     const char *name() const {  // MainOp::name (kernel.rs:1499-1515)
         switch (kind) {
+        case BL_MAIN_CONV3X3: return "conv2d3x3";
+        case BL_MAIN_CONV_TRANSPOSE: return "conv_transpose2d";
+        case BL_MAIN_RESIZE_BILINEAR: return "resize_bilinear";
         case BL_MAIN_LAYER_NORM: return "layernorm";
         case BL_MAIN_MATMUL: return "matmul";
         case BL_MAIN_PATCH_EMBED: return "patch_embed";
@@ -174,6 +202,9 @@ struct MainOp {
         case BL_MAIN_LAYER_NORM: case BL_MAIN_SOFTMAX: case BL_MAIN_MATMUL: return d[0];
         case BL_MAIN_PATCH_EMBED: return (uint32_t)std::min<uint64_t>(product({d[0], d[1]}), UINT32_MAX);
         case BL_MAIN_ATTENTION_SCORES: case BL_MAIN_ATTENTION_VALUES: case BL_MAIN_FLASH_ATTENTION: return d[0];
+        case BL_MAIN_CONV3X3: return (uint32_t)std::min<uint64_t>(product({strided(d[0], d[4]), strided(d[1], d[4])}), UINT32_MAX);
+        case BL_MAIN_CONV_TRANSPOSE: return (uint32_t)std::min<uint64_t>(product({d[0], d[4], d[1], d[4]}), UINT32_MAX);
+        case BL_MAIN_RESIZE_BILINEAR: return (uint32_t)std::min<uint64_t>(product({d[2], d[3]}), UINT32_MAX);
         default: return (uint32_t)std::min<uint64_t>(output_elements(), UINT32_MAX);
         }
     }
@@ -184,6 +215,7 @@ struct MainOp {
         case BL_MAIN_PATCH_EMBED: cols = d[4]; layers = 1; return true;
         case BL_MAIN_ATTENTION_SCORES: cols = d[0]; layers = d[1]; return true;
         case BL_MAIN_ATTENTION_VALUES: cols = d[2]; layers = d[1]; return true;
+        case BL_MAIN_CONV3X3: cols = d[3]; layers = 1; return true;
         default: return false;
         }
     }
@@ -204,6 +236,8 @@ struct MainOp {
         case BL_MAIN_PATCH_EMBED: return d[4];
         case BL_MAIN_ATTENTION_SCORES: return product({d[1], d[0]});
         case BL_MAIN_ATTENTION_VALUES: case BL_MAIN_FLASH_ATTENTION: return product({d[1], d[2]});
+        case BL_MAIN_CONV3X3: case BL_MAIN_CONV_TRANSPOSE: return d[3];
+        case BL_MAIN_RESIZE_BILINEAR: return d[4];
         default: return 1;
         }
     }
@@ -262,6 +296,25 @@ void standalone(const bli_op &o, MainOp &m, std::vector<Epi> &e) {
     case BLI_OP_ATTENTION_SCORES: m.kind = BL_MAIN_ATTENTION_SCORES; m.t[0] = t[0]; m.d[0] = d[0]; m.d[1] = d[1]; m.d[2] = d[2]; break;
     case BLI_OP_SOFTMAX: m.kind = BL_MAIN_SOFTMAX; m.t[0] = t[0]; m.d[0] = d[0]; m.d[1] = d[1]; break;
     case BLI_OP_ATTENTION_VALUES: m.kind = BL_MAIN_ATTENTION_VALUES; m.t[0] = t[0]; m.t[1] = t[1]; m.d[0] = d[0]; m.d[1] = d[1]; m.d[2] = d[2]; break;
+    case BLI_OP_CONV3X3:
+        m.kind = BL_MAIN_CONV3X3; m.t[0] = t[0]; m.t[1] = t[1]; m.t[2] = t[2];
+        for (int i = 0; i < 5; i++) m.d[i] = d[i];
+        m.d[5] = t[2] != BLI_NONE;
+        break;
+    case BLI_OP_CONV1X1:  // Conv2d1x1::as_matmul (kernel.rs:531-545): the [pixels][cin] image times [cin][cout]
+        m.kind = BL_MAIN_MATMUL; m.t[0] = t[0]; m.t[1] = t[1]; m.t[2] = t[2];
+        m.d[0] = (uint32_t)std::min<uint64_t>(product({d[0], d[1]}), UINT32_MAX); m.d[1] = d[2]; m.d[2] = d[3];
+        m.d[3] = t[2] != BLI_NONE;
+        break;
+    case BLI_OP_CONV_TRANSPOSE:
+        m.kind = BL_MAIN_CONV_TRANSPOSE; m.t[0] = t[0]; m.t[1] = t[1]; m.t[2] = t[2];
+        for (int i = 0; i < 5; i++) m.d[i] = d[i];
+        m.d[5] = t[2] != BLI_NONE;
+        break;
+    case BLI_OP_RESIZE_BILINEAR:
+        m.kind = BL_MAIN_RESIZE_BILINEAR; m.t[0] = t[0];
+        for (int i = 0; i < 5; i++) m.d[i] = d[i];
+        break;
     case BLI_OP_ADD: map(t[0], d[0]); e.push_back({BL_EPI_ADD, t[1]}); break;
     case BLI_OP_RELU: map(t[0], d[0]); e.push_back({BL_EPI_RELU}); break;
     case BLI_OP_GELU: map(t[0], d[0]); e.push_back({BL_EPI_GELU}); break;
@@ -298,6 +351,7 @@ struct Spec {
     uint32_t output = BLI_NONE;
     uint32_t op_begin = 0, op_end = 0;
     uint32_t part_index = 0, part_count = 1, part_start = 0, part_end = 0;
+    uint32_t prologue = 0;  // BL_PRO_* applied to the main input as it is loaded (kernel.rs:1639-1659)
 
     static Spec whole_of(const MainOp &m, const std::vector<Epi> &e, uint32_t out, uint32_t b, uint32_t en) {
         Spec s;
@@ -310,7 +364,11 @@ struct Spec {
         s.part_end = m.split_extent();
         return s;
     }
-    Spec whole() const { return whole_of(main, epilogue, output, op_begin, op_end); }
+    Spec whole() const {
+        Spec w = whole_of(main, epilogue, output, op_begin, op_end);
+        w.prologue = prologue;
+        return w;
+    }
     bool is_whole() const { return part_count == 1; }
     uint32_t max_parts() const {  // kernel.rs:1966-1969
         uint32_t g = main.split_grain();
@@ -328,8 +386,9 @@ struct Spec {
         out.push_back(output);
         return out;
     }
-    std::string name() const {
-        std::string n = main.name();
+    std::string name() const {  // KernelSpec::name (kernel.rs:2119-2131): prologue-main+epilogue
+        std::string n = prologue == BL_PRO_RELU ? "relu-" : "";
+        n += main.name();
         for (const Epi &e : epilogue) {
             n += "+";
             n += epi_name(e.kind);
@@ -565,6 +624,21 @@ extern "C" int bli_graph_lower(const bli_graph *g, uint32_t fusion, bli_program 
     for (const auto &[op, o] : g->ops)
         for (auto &r : op_reads(op)) consumers[r.first]++;
     std::vector<Spec> kernels;
+    // relu_prologue (kernel.rs:1381-1402): a ReLU whose output is an
+    // activation read once, by the 3x3 convolution right after it as its
+    // image, becomes that convolution's prologue; the convolution binds the
+    // ReLU's input instead.
+    auto relu_prologue = [&](uint32_t index) {
+        const bli_op &op = g->ops[index].first;
+        if (op.kind != BLI_OP_RELU || index + 1 >= g->ops.size()) return false;
+        const uint32_t relu = g->ops[index].second;
+        const bli_op &next = g->ops[index + 1].first;
+        auto role = g->tensors.find(relu);
+        return next.kind == BLI_OP_CONV3X3 && next.t[0] == relu && role != g->tensors.end() &&
+               role->second.role == BLI_ACTIVATION && consumers[relu] == 1;
+    };
+    bool deferred = false;
+    uint32_t deferred_at = 0, deferred_input = BLI_NONE;
     for (uint32_t index = 0; index < g->ops.size(); index++) {
         const bli_op &op = g->ops[index].first;
         const uint32_t output = g->ops[index].second;
@@ -586,10 +660,24 @@ extern "C" int bli_graph_lower(const bli_graph *g, uint32_t fusion, bli_program 
                 }
             }
         }
+        if (fusion == BLI_FUSION_ON && relu_prologue(index)) {
+            deferred = true;
+            deferred_at = index;
+            deferred_input = op.t[0];
+            continue;
+        }
         MainOp m;
         std::vector<Epi> e;
         standalone(op, m, e);
-        kernels.push_back(Spec::whole_of(m, e, output, index, index + 1));
+        uint32_t start = index, prologue = 0;
+        if (deferred) {
+            m.t[0] = deferred_input;
+            prologue = BL_PRO_RELU;
+            start = deferred_at;
+            deferred = false;
+        }
+        kernels.push_back(Spec::whole_of(m, e, output, start, index + 1));
+        kernels.back().prologue = prologue;
     }
     for (const Spec &s : kernels)
         if (int r = check_spec(s, BASELINE)) return r;
@@ -702,6 +790,7 @@ extern "C" int bli_program_kernel(const bli_program *p, uint32_t k, bli_kernel_i
     for (size_t i = 0; i < b.size() && i < BL_MAX_BINDINGS; i++) out->bindings[i] = b[i];
     out->first_op = s.op_begin;
     out->end_op = s.op_end;
+    out->prologue = s.prologue;
     return 0;
 }
 
@@ -749,6 +838,7 @@ extern "C" int bli_program_spec(const bli_program *p, uint32_t k, const bli_plan
     out->n_epilogue = info.n_epilogue;
     memcpy(out->epilogue, info.epilogue, sizeof out->epilogue);
     out->n_bindings = info.n_bindings;
+    out->prologue = info.prologue;
     const uint32_t dtype = program_dtype(p);
     for (uint32_t b = 0; b < info.n_bindings; b++) {
         auto it = plan->placements.find(info.bindings[b]);

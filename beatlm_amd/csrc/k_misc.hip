@@ -349,6 +349,59 @@ __global__ __launch_bounds__(256) void element_kernel(ElementArgs a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// The DPT head's gathers, one output element per invocation.
+//
+// Transposed convolution, kernel = stride = f (ConvTranspose2d,
+// kernel.rs:547-597): output pixel (Y, X) lies in the f x f block of input
+// pixel (Y / f, X / f) at tap (Y % f, X % f), and no other input pixel reaches
+// it, so each output element is the bias plus one dot product over the input
+// channels (the reference's own kernel gathers the same way). Lanes of a wave
+// take consecutive output channels: the input pixel is shared, the HWIO
+// weight reads are contiguous.
+//
+// Bilinear resampling with aligned corners (ResizeBilinear,
+// kernel.rs:599-631): positions as PyTorch's interpolate computes them in f32,
+// ratio * index, the floor and the next index clamped to the last row or
+// column, weights 1 - l and l.
+// ------------------------------------------------------------------------
+template <Dpt K, typename T>
+__global__ __launch_bounds__(256) void dpt_kernel(DptArgs a) {
+    const T *X = (const T *)a.x;
+    T *Y = (T *)a.y;
+    for (uint64_t i = a.start + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < a.end;
+         i += (uint64_t)gridDim.x * 256) {
+        float v;
+        if constexpr (K == Dpt::CONV_TRANSPOSE) {
+            const uint32_t w = a.d[1], cin = a.d[2], cout = a.d[3], f = a.d[4];
+            const uint64_t pixel = i / cout;
+            const uint32_t co = (uint32_t)(i % cout);
+            const uint32_t ow = w * f;
+            const uint32_t oy = (uint32_t)(pixel / ow), ox = (uint32_t)(pixel % ow);
+            const uint32_t y = oy / f, ky = oy % f, x = ox / f, kx = ox % f;
+            const T *in = X + ((uint64_t)y * w + x) * cin;
+            const T *wt = (const T *)a.w + ((uint64_t)(ky * f + kx) * cin) * cout + co;
+            float acc = 0.0f;
+            for (uint32_t ci = 0; ci < cin; ci++) acc += to_f32(in[ci]) * to_f32(wt[(uint64_t)ci * cout]);
+            v = acc + (a.d[5] ? to_f32(((const T *)a.bias)[co]) : 0.0f);
+        } else {
+            const uint32_t ih = a.d[0], iw = a.d[1], ow = a.d[3], c = a.d[4];
+            const uint64_t pixel = i / c;
+            const uint32_t ch = (uint32_t)(i % c);
+            const uint32_t oy = (uint32_t)(pixel / ow), ox = (uint32_t)(pixel % ow);
+            const float py = a.ry * (float)oy, px = a.rx * (float)ox;
+            const uint32_t y0 = min((uint32_t)py, ih - 1), x0 = min((uint32_t)px, iw - 1);
+            const uint32_t y1 = min(y0 + 1, ih - 1), x1 = min(x0 + 1, iw - 1);
+            const float ly = py - (float)y0, lx = px - (float)x0;
+            auto at = [&](uint32_t yy, uint32_t xx) { return to_f32(X[((uint64_t)yy * iw + xx) * c + ch]); };
+            const float top = (1.0f - lx) * at(y0, x0) + lx * at(y0, x1);
+            const float bottom = (1.0f - lx) * at(y1, x0) + lx * at(y1, x1);
+            v = (1.0f - ly) * top + ly * bottom;
+        }
+        Y[i] = from_f32<T>(apply_epilogue<T>(a.epi, v, i));
+    }
+}
+
 // Spins until `ticks` of the device's constant-rate wall clock have passed.
 __global__ void spin_kernel(uint64_t ticks) {
     const uint64_t t0 = wall_clock64();
@@ -399,6 +452,20 @@ hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStrea
     default: BL_ELEM(PerElement::DROP_FIRST) break;
     }
 #undef BL_ELEM
+    return hipGetLastError();
+}
+
+hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s) {
+    if (a.end <= a.start) return hipSuccess;
+    uint64_t blocks = (a.end - a.start + 255) / 256;
+    if (blocks > 65535) blocks = 65535;
+    dim3 grid((uint32_t)blocks);
+#define BL_DPT(K)                                                                      \
+    if (f16) hipLaunchKernelGGL((dpt_kernel<K, _Float16>), grid, dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((dpt_kernel<K, float>), grid, dim3(256), 0, s, a);
+    if (k == Dpt::CONV_TRANSPOSE) { BL_DPT(Dpt::CONV_TRANSPOSE) }
+    else { BL_DPT(Dpt::RESIZE) }
+#undef BL_DPT
     return hipGetLastError();
 }
 

@@ -50,7 +50,8 @@ struct GemmArgs {
     uint32_t kgroups;     // pipelined kernel: groups of 4 waves splitting the k-steps (1, 2 or 4)
     uint32_t stages;      // pipelined kernel: ring depth per group (2 .. 4)
     uint32_t kslices;     // pipelined kernel: 32-wide k-slices per ring stage (1 or 2)
-    uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width
+    uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width; conv3x3: height, width, cin, stride
+    uint32_t p4, p5;          // conv3x3: output width, ReLU prologue (1) or none (0)
     EpilogueArgs epi;
     // The QKV projection of a flash attention kernel also writes that
     // kernel's K [planes][H][t_pad][64] and Vt [planes][H][64][t_pad]
@@ -120,6 +121,19 @@ struct FlashPlan {
     uint64_t scratch_bytes = 0;
 };
 
+// The DPT head's gathers: each output element from a few input values.
+enum class Dpt : int { CONV_TRANSPOSE = 0, RESIZE = 1 };
+
+struct DptArgs {
+    const void *x, *w, *bias;
+    void *y;
+    uint32_t d[6];        // conv transpose: height, width, cin, cout, factor, has_bias;
+                          // resize: in_height, in_width, out_height, out_width, channels
+    float ry, rx;         // resize: input rows (columns) per output row (column), as PyTorch computes them
+    uint64_t start, end;  // output elements of the part
+    EpilogueArgs epi;
+};
+
 // One element per invocation: the standalone map, the token copies.
 enum class PerElement : int { MAP = 0, PREPEND = 1, DROP_FIRST = 2 };
 
@@ -160,6 +174,7 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
 void bind_flash_scratch(FlashArgs &a, Math m, void *base);
 hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s);
 hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
+hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s);
 
 // GEMM tile shapes the dispatcher can pick from: BM x BN.
 enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_COUNT = 4 };

@@ -45,7 +45,11 @@ MAIN_PATCH_EMBED = 6
 MAIN_PREPEND_TOKEN = 7
 MAIN_TOKENS_TO_MAP = 8
 MAIN_MAP = 9
+MAIN_CONV3X3 = 10
+MAIN_CONV_TRANSPOSE = 11
+MAIN_RESIZE_BILINEAR = 12
 MAIN_FLASH_ATTENTION = 100
+PRO_RELU = 1
 
 # epilogue steps
 EPI_ADD = 1
@@ -94,6 +98,7 @@ class Spec(C.Structure):
         ("epilogue", Epilogue * MAX_EPILOGUE),
         ("n_bindings", C.c_uint32),
         ("bindings", Binding * MAX_BINDINGS),
+        ("prologue", C.c_uint32),
     ]
 
 

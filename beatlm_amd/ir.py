@@ -28,6 +28,10 @@ OP_ATTENTION_VALUES = 5
 OP_PATCH_EMBED = 6
 OP_PREPEND_TOKEN = 7
 OP_TOKENS_TO_MAP = 8
+OP_CONV3X3 = 9
+OP_CONV1X1 = 10
+OP_CONV_TRANSPOSE = 11
+OP_RESIZE_BILINEAR = 12
 OP_ADD = 20
 OP_RELU = 21
 OP_GELU = 22
@@ -107,6 +111,7 @@ class KernelInfo(C.Structure):
         ("bindings", C.c_uint32 * hip.MAX_BINDINGS),
         ("first_op", C.c_uint32),
         ("end_op", C.c_uint32),
+        ("prologue", C.c_uint32),
     ]
 
 
@@ -304,6 +309,154 @@ def vit_encoder(
         features.append(fmap)
         nid += 2
     return EncoderIds(emb, blocks, final_g, final_b, features, nid)
+
+
+@dataclass(frozen=True)
+class DepthConfig:
+    """The structure of a Depth Anything V2 model
+    (crates/beatlm/src/load/depth_anything_v2.rs:85-152); `small()` is
+    depth-anything/Depth-Anything-V2-Small-hf. `reassemble` per stage:
+    ("up", f) a transposed convolution of kernel and stride f, ("keep",) or
+    ("down", f) a 3x3 convolution at stride f."""
+
+    image_size: int = 518
+    patch_size: int = 14
+    num_channels: int = 3
+    hidden_size: int = 384
+    num_layers: int = 12
+    num_heads: int = 6
+    mlp_ratio: int = 4
+    out_indices: tuple = (3, 6, 9, 12)
+    neck_hidden_sizes: tuple = (48, 96, 192, 384)
+    reassemble: tuple = (("up", 4), ("up", 2), ("keep",), ("down", 2))
+    fusion_hidden_size: int = 64
+    head_hidden_size: int = 32
+    eps: float = 1e-6
+
+    @classmethod
+    def small(cls) -> "DepthConfig":
+        return cls()
+
+
+class _Ids:
+    """Tensor ids handed out in order, as the reference's Builder does
+    (crates/beatlm/src/model/mod.rs:360-444): every weight when an operation
+    first needs it, then the operation's output."""
+
+    def __init__(self, g: "Graph", first_id: int):
+        self.g, self.next = g, first_id
+        self.weights = []  # (id, name, elements) in declaration order
+
+    def weight(self, name: str, elements: int) -> int:
+        tid = self.next
+        self.next += 1
+        self.g.tensor(tid, WEIGHT, elements)
+        self.weights.append((tid, name, elements))
+        return tid
+
+    def op(self, o: Op, role: int = ACTIVATION) -> int:
+        tid = self.next
+        self.next += 1
+        self.g.tensor(tid, role, output_elements(o))
+        self.g.push(o, tid)
+        return tid
+
+
+def _conv3x3(ids, x, name, size, cin, cout, stride=1, bias=True, role=ACTIVATION):
+    w = ids.weight(name + ".weight", 9 * cin * cout)
+    b = ids.weight(name + ".bias", cout) if bias else NONE
+    return ids.op(op(OP_CONV3X3, [x, w, b], [size[0], size[1], cin, cout, stride]), role)
+
+
+def _conv1x1(ids, x, name, size, cin, cout, role=ACTIVATION):
+    w = ids.weight(name + ".weight", cin * cout)
+    b = ids.weight(name + ".bias", cout)
+    return ids.op(op(OP_CONV1X1, [x, w, b], [size[0], size[1], cin, cout]), role)
+
+
+def _strided(extent, stride):
+    return (extent - 1) // stride + 1
+
+
+def _residual_unit(ids, x, name, size, c):
+    """x + conv2(relu(conv1(relu(x)))): depth_anything_v2.rs:776-812."""
+    n = size[0] * size[1] * c
+    a = ids.op(op(OP_RELU, [x], [n]))
+    first = _conv3x3(ids, a, name + ".convolution1", size, c, c)
+    a2 = ids.op(op(OP_RELU, [first], [n]))
+    second = _conv3x3(ids, a2, name + ".convolution2", size, c, c)
+    return ids.op(op(OP_ADD, [second, x], [n]))
+
+
+def depth_decoder(g: "Graph", cfg: DepthConfig, side: int, features, first_id: int, depth_role: int = OUTPUT):
+    """The reference's decoder() (depth_anything_v2.rs:882-981): per stage a
+    1x1 projection and its resampling, then a 3x3 convolution to the fusion
+    width; the fusion layers deepest stage first (residual units, resampling,
+    1x1 projection); the head (3x3, resample to the image side, 3x3 + ReLU,
+    1x1 to one channel + ReLU). Returns (depth id, weights [(id, name,
+    elements)], next id); depth is [side][side]."""
+    ids = _Ids(g, first_id)
+    grid = side // cfg.patch_size
+    fusion = cfg.fusion_hidden_size
+    stages = []
+    for i, feat in enumerate(features):
+        ch = cfg.neck_hidden_sizes[i]
+        proj = _conv1x1(ids, feat, f"neck.reassemble_stage.layers.{i}.projection", (grid, grid), cfg.hidden_size, ch)
+        kind = cfg.reassemble[i]
+        if kind[0] == "up":
+            f = kind[1]
+            w = ids.weight(f"neck.reassemble_stage.layers.{i}.resize.weight", f * f * ch * ch)
+            b = ids.weight(f"neck.reassemble_stage.layers.{i}.resize.bias", ch)
+            m = ids.op(op(OP_CONV_TRANSPOSE, [proj, w, b], [grid, grid, ch, ch, f]))
+            hw = (grid * f, grid * f)
+        elif kind[0] == "down":
+            m = _conv3x3(ids, proj, f"neck.reassemble_stage.layers.{i}.resize", (grid, grid), ch, ch, kind[1])
+            hw = (_strided(grid, kind[1]), _strided(grid, kind[1]))
+        else:
+            m, hw = proj, (grid, grid)
+        stages.append((_conv3x3(ids, m, f"neck.convs.{i}", hw, ch, fusion, bias=False), hw))
+    fused = None
+    for layer, (stage, hw) in enumerate(reversed(stages)):
+        nxt = len(stages) - (layer + 2)
+        out = stages[nxt][1] if nxt >= 0 else (hw[0] * 2, hw[1] * 2)
+        name = f"neck.fusion_stage.layers.{layer}"
+        x = stage
+        n = hw[0] * hw[1] * fusion
+        if fused is not None:
+            unit = _residual_unit(ids, stage, name + ".residual_layer1", hw, fusion)
+            x = ids.op(op(OP_ADD, [unit, fused[0]], [n]))
+        x = _residual_unit(ids, x, name + ".residual_layer2", hw, fusion)
+        resized = ids.op(op(OP_RESIZE_BILINEAR, [x], [hw[0], hw[1], out[0], out[1], fusion]))
+        fused = (_conv1x1(ids, resized, name + ".projection", out, fusion, fusion), out)
+    x, hw = fused
+    half, width, full = fusion // 2, cfg.head_hidden_size, grid * cfg.patch_size
+    first = _conv3x3(ids, x, "head.conv1", hw, fusion, half)
+    resized = ids.op(op(OP_RESIZE_BILINEAR, [first], [hw[0], hw[1], full, full, half]))
+    second = _conv3x3(ids, resized, "head.conv2", (full, full), half, width)
+    act = ids.op(op(OP_RELU, [second], [full * full * width]))
+    third = _conv1x1(ids, act, "head.conv3", (full, full), width, 1)
+    depth = ids.op(op(OP_RELU, [third], [full * full]), depth_role)
+    return depth, ids.weights, ids.next
+
+
+@dataclass
+class DepthModelIds:
+    encoder: "EncoderIds"
+    depth: int
+    decoder_weights: list
+    next_id: int
+
+
+def depth_model(g: "Graph", cfg: DepthConfig, side: int | None = None, first_id: int = 0) -> DepthModelIds:
+    """The reference's model() (depth_anything_v2.rs:984-995): the encoder,
+    its features as activations, and the decoder reading them; the depth is
+    the output."""
+    side = side or cfg.image_size
+    grid = side // cfg.patch_size
+    enc = vit_encoder(g, grid, cfg.patch_size, cfg.num_channels, cfg.hidden_size, cfg.num_heads,
+                      cfg.hidden_size * cfg.mlp_ratio, cfg.eps, cfg.out_indices, first_id, ACTIVATION)
+    depth, weights, nid = depth_decoder(g, cfg, side, enc.features, enc.next_id)
+    return DepthModelIds(enc, depth, weights, nid)
 
 
 def output_elements(o: Op) -> int:

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define BL_ABI_VERSION 1u
+#define BL_ABI_VERSION 2u
 #define BL_MAX_EPILOGUE 8
 #define BL_MAX_BINDINGS 8
 
@@ -84,6 +84,13 @@ enum {
     BL_MAIN_PREPEND_TOKEN = 7,    /* dims: rows, channels */
     BL_MAIN_TOKENS_TO_MAP = 8,    /* dims: height, width, channels */
     BL_MAIN_MAP = 9,              /* dims: elements */
+    /* The DPT head's operations (kernel.rs:447-631). */
+    BL_MAIN_CONV3X3 = 10,         /* dims: height, width, cin, cout, stride, has_bias; NHWC, HWIO weights, padding 1;
+                                   * split along output pixels; prologue BL_PRO_RELU allowed */
+    BL_MAIN_CONV_TRANSPOSE = 11,  /* dims: height, width, cin, cout, factor, has_bias; kernel = stride = factor;
+                                   * split along output pixels */
+    BL_MAIN_RESIZE_BILINEAR = 12, /* dims: in_height, in_width, out_height, out_width, channels; corners aligned;
+                                   * split along output pixels */
     /* Backend-level main op with no MainOp counterpart: the three kernels
      * attention_scores+scale -> softmax -> attention_values over one qkv tensor
      * fused into one flash-attention kernel (online softmax, no [T][H][T]
@@ -91,6 +98,10 @@ enum {
      * factor. Bindings: qkv, output. Parts split along query rows. */
     BL_MAIN_FLASH_ATTENTION = 100
 };
+
+/* ---- prologue steps (Prologue, kernel.rs:1639-1659): applied to every
+ * value of the main input as it is loaded; only BL_MAIN_CONV3X3 takes one ---- */
+enum { BL_PRO_RELU = 1 };
 
 /* ---- epilogue steps (Epilogue, kernel.rs:1593-1615) ---- */
 enum {
@@ -147,6 +158,7 @@ typedef struct {
     bl_epilogue epilogue[BL_MAX_EPILOGUE];
     uint32_t n_bindings;
     bl_binding bindings[BL_MAX_BINDINGS];
+    uint32_t prologue;             /* BL_PRO_* or 0 (KernelSpec::prologue, kernel.rs:1947) */
 } bl_spec;
 
 /* One binding set: tensors of the specs bound to stand-ins (Substitution,

@@ -45,8 +45,12 @@ extern "C" {
 enum { BLI_INPUT = 0, BLI_WEIGHT = 1, BLI_ACTIVATION = 2, BLI_OUTPUT = 3 }; /* TensorRole */
 enum { BLI_FUSION_ON = 0, BLI_FUSION_OFF = 1 };                              /* Fusion */
 
-/* OpKind (kernel.rs:818-916), the variants of the encoder block. */
+/* OpKind (kernel.rs:818-916): the encoder block's variants and the DPT head's. */
 enum {
+    BLI_OP_CONV3X3 = 9,          /* t: image, weights [3][3][cin][cout], bias|NONE; d: height, width, cin, cout, stride */
+    BLI_OP_CONV1X1 = 10,         /* t: image, weights [cin][cout], bias|NONE; d: height, width, cin, cout */
+    BLI_OP_CONV_TRANSPOSE = 11,  /* t: image, weights [f][f][cin][cout], bias|NONE; d: height, width, cin, cout, factor */
+    BLI_OP_RESIZE_BILINEAR = 12, /* t: map; d: in_height, in_width, out_height, out_width, channels */
     BLI_OP_LAYER_NORM = 1,       /* t: input, gamma, beta; d: rows, channels; f: epsilon */
     BLI_OP_MATMUL = 2,           /* t: a, b, bias|NONE; d: m, k, n */
     BLI_OP_ATTENTION_SCORES = 3, /* t: qkv; d: tokens, heads, head_dim */
@@ -144,6 +148,7 @@ typedef struct {
     uint32_t n_bindings;
     uint32_t bindings[BL_MAX_BINDINGS];      /* tensor ids, output last */
     uint32_t first_op, end_op;               /* KernelSpec::ops */
+    uint32_t prologue;                       /* BL_PRO_* or 0 */
 } bli_kernel_info;
 
 typedef struct bli_graph bli_graph;

@@ -62,6 +62,10 @@ def lib():
             "blo_ref_attention": [_F, _S, _S, _S, C.c_float, _F],
             "blo_ref_patch_embed": [_F, _F, _F, _S, _S, _S, _S, _S, _F],
             "blo_ref_prepend_token": [_F, _F, _S, _S, _F],
+            "blo_ref_conv3x3": [_F, _F, _F, _S, _S, _S, _S, _S, _F],
+            "blo_ref_conv1x1": [_F, _F, _F, _S, _S, _S, _F],
+            "blo_ref_conv_transpose": [_F, _F, _F, _S, _S, _S, _S, _S, _F],
+            "blo_ref_resize_bilinear": [_F, _S, _S, _S, _S, _S, _F],
             "blo_ref_vit_block": [_F, C.POINTER(BlockWeights), _S, _S, _S, _S, C.c_float, C.c_int, _F],
             "blo_wg_layernorm": [_F, _F, _F, _S, _S, C.c_float, _F],
             "blo_wg_softmax": [_F, _S, _S, _F],
@@ -219,6 +223,43 @@ def prepend_token(token, tokens, rows, c):
     token, tokens = _f32(token), _f32(tokens)
     out = np.empty((rows + 1) * c, np.float32)
     lib().blo_ref_prepend_token(_p(token), _p(tokens), rows, c, _p(out))
+    return out
+
+
+def _opt(bias):
+    return _f32(bias) if bias is not None else None
+
+
+def conv3x3(x, w, bias, h, wd, cin, cout, stride=1):
+    """reference.rs:31-81: NHWC x, HWIO w [3][3][cin][cout], padding 1."""
+    x, w, b = _f32(x), _f32(w), _opt(bias)
+    oh, ow = (h - 1) // stride + 1, (wd - 1) // stride + 1
+    out = np.empty(oh * ow * cout, np.float32)
+    lib().blo_ref_conv3x3(_p(x), _p(w), _p(b) if b is not None else None, h, wd, cin, cout, stride, _p(out))
+    return out
+
+
+def conv1x1(x, w, bias, pixels, cin, cout):
+    """reference.rs:87-106."""
+    x, w, b = _f32(x), _f32(w), _opt(bias)
+    out = np.empty(pixels * cout, np.float32)
+    lib().blo_ref_conv1x1(_p(x), _p(w), _p(b) if b is not None else None, pixels, cin, cout, _p(out))
+    return out
+
+
+def conv_transpose(x, w, bias, h, wd, cin, cout, f):
+    """reference.rs:114-144: kernel = stride = f, HWIO w [f][f][cin][cout]."""
+    x, w, b = _f32(x), _f32(w), _opt(bias)
+    out = np.empty(h * f * wd * f * cout, np.float32)
+    lib().blo_ref_conv_transpose(_p(x), _p(w), _p(b) if b is not None else None, h, wd, cin, cout, f, _p(out))
+    return out
+
+
+def resize_bilinear(x, ih, iw, oh, ow, c):
+    """reference.rs:151-179: aligned corners."""
+    x = _f32(x)
+    out = np.empty(oh * ow * c, np.float32)
+    lib().blo_ref_resize_bilinear(_p(x), ih, iw, oh, ow, c, _p(out))
     return out
 
 

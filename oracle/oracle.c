@@ -305,6 +305,94 @@ void blo_ref_patch_embed(const float *image, const float *w, const float *bias,
     }
 }
 
+/* reference.rs:43-81: every output pixel centred on input (y s, x s); a tap
+ * outside the image reads zero. Sum in f64 in (ky, kx, ci) order after the bias. */
+void blo_ref_conv3x3(const float *in, const float *w, const float *bias, size_t h,
+                     size_t wd, size_t cin, size_t cout, size_t stride, float *out) {
+    const size_t oh = (h - 1) / stride + 1, ow = (wd - 1) / stride + 1;
+    #pragma omp parallel for schedule(static)
+    for (size_t px = 0; px < oh * ow; px++) {
+        const size_t y = px / ow, x = px % ow;
+        for (size_t co = 0; co < cout; co++) {
+            double acc = bias ? (double)bias[co] : 0.0;
+            for (size_t ky = 0; ky < 3; ky++)
+                for (size_t kx = 0; kx < 3; kx++) {
+                    if (y * stride + ky < 1 || x * stride + kx < 1) continue;
+                    const size_t iy = y * stride + ky - 1, ix = x * stride + kx - 1;
+                    if (iy >= h || ix >= wd) continue;
+                    const float *a = in + (iy * wd + ix) * cin;
+                    const float *b = w + (ky * 3 + kx) * cin * cout + co;
+                    for (size_t ci = 0; ci < cin; ci++) acc += (double)a[ci] * (double)b[ci * cout];
+                }
+            out[px * cout + co] = (float)acc;
+        }
+    }
+}
+
+/* reference.rs:87-106. */
+void blo_ref_conv1x1(const float *in, const float *w, const float *bias, size_t pixels,
+                     size_t cin, size_t cout, float *out) {
+    #pragma omp parallel for schedule(static)
+    for (size_t p = 0; p < pixels; p++)
+        for (size_t co = 0; co < cout; co++) {
+            double acc = bias ? (double)bias[co] : 0.0;
+            for (size_t ci = 0; ci < cin; ci++) acc += (double)in[p * cin + ci] * (double)w[ci * cout + co];
+            out[p * cout + co] = (float)acc;
+        }
+}
+
+/* reference.rs:114-144: every input pixel adds its channels times each tap
+ * into the output pixel the tap reaches, accumulated in f64; then the bias. */
+void blo_ref_conv_transpose(const float *in, const float *w, const float *bias, size_t h,
+                            size_t wd, size_t cin, size_t cout, size_t f, float *out) {
+    const size_t ow = wd * f, total = h * f * ow * cout;
+    double *acc = (double *)calloc(total, sizeof(double));
+    for (size_t y = 0; y < h; y++)
+        for (size_t x = 0; x < wd; x++)
+            for (size_t ky = 0; ky < f; ky++)
+                for (size_t kx = 0; kx < f; kx++) {
+                    double *o = acc + ((y * f + ky) * ow + x * f + kx) * cout;
+                    for (size_t ci = 0; ci < cin; ci++) {
+                        const double v = in[(y * wd + x) * cin + ci];
+                        const float *taps = w + ((ky * f + kx) * cin + ci) * cout;
+                        for (size_t co = 0; co < cout; co++) o[co] += v * (double)taps[co];
+                    }
+                }
+    for (size_t i = 0; i < total; i++) out[i] = (float)(acc[i] + (bias ? (double)bias[i % cout] : 0.0));
+    free(acc);
+}
+
+/* reference.rs:151-179: position o (in - 1) / (out - 1) (zero for one output),
+ * the floor and the next index clamped to the last, weights in f64. */
+static void resize_axis(size_t o, size_t in, size_t outn, size_t *i0, size_t *i1, double *l) {
+    const double pos = outn > 1 ? (double)o * (double)(in - 1) / (double)(outn - 1) : 0.0;
+    size_t f = (size_t)floor(pos);
+    if (f > in - 1) f = in - 1;
+    *i0 = f;
+    *i1 = f + 1 < in ? f + 1 : in - 1;
+    *l = pos - (double)f;
+}
+void blo_ref_resize_bilinear(const float *in, size_t ih, size_t iw, size_t oh, size_t ow,
+                             size_t c, float *out) {
+    #pragma omp parallel for schedule(static)
+    for (size_t oy = 0; oy < oh; oy++) {
+        size_t y0, y1;
+        double ly;
+        resize_axis(oy, ih, oh, &y0, &y1, &ly);
+        for (size_t ox = 0; ox < ow; ox++) {
+            size_t x0, x1;
+            double lx;
+            resize_axis(ox, iw, ow, &x0, &x1, &lx);
+            for (size_t ch = 0; ch < c; ch++) {
+                const double a = in[(y0 * iw + x0) * c + ch], b = in[(y0 * iw + x1) * c + ch];
+                const double cc = in[(y1 * iw + x0) * c + ch], d = in[(y1 * iw + x1) * c + ch];
+                const double top = (1.0 - lx) * a + lx * b, bottom = (1.0 - lx) * cc + lx * d;
+                out[(oy * ow + ox) * c + ch] = (float)((1.0 - ly) * top + ly * bottom);
+            }
+        }
+    }
+}
+
 /* reference.rs:423-425. */
 void blo_ref_prepend_token(const float *token, const float *tokens, size_t rows,
                            size_t c, float *out) {

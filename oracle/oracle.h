@@ -67,6 +67,22 @@ void blo_ref_patch_embed(const float *image, const float *w, const float *bias,
 void blo_ref_prepend_token(const float *token, const float *tokens, size_t rows,
                            size_t c, float *out);                     /* :423-425 */
 
+/* The DPT head's operations, NHWC maps and HWIO weights (reference.rs:26-191). */
+/* 3x3 convolution, zero padding 1, at `stride`: output [oh][ow][cout] with
+ * oh = (h - 1) / stride + 1; bias may be NULL.                    :31-81 */
+void blo_ref_conv3x3(const float *in, const float *w, const float *bias, size_t h,
+                     size_t wd, size_t cin, size_t cout, size_t stride, float *out);
+/* 1x1 convolution: [pixels][cin] times [cin][cout], per pixel.        :87-106 */
+void blo_ref_conv1x1(const float *in, const float *w, const float *bias, size_t pixels,
+                     size_t cin, size_t cout, float *out);
+/* Transposed convolution, kernel = stride = f, no padding, written as its
+ * scatter definition: output [h f][w f][cout].                       :114-144 */
+void blo_ref_conv_transpose(const float *in, const float *w, const float *bias, size_t h,
+                            size_t wd, size_t cin, size_t cout, size_t f, float *out);
+/* Bilinear resampling with aligned corners, f64 positions.          :151-179 */
+void blo_ref_resize_bilinear(const float *in, size_t ih, size_t iw, size_t oh, size_t ow,
+                             size_t c, float *out);
+
 /* The weights of one block in the IR's layouts (reference.rs:497-516). */
 typedef struct {
     const float *norm1_g, *norm1_b;

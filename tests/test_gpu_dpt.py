@@ -1,0 +1,234 @@
+"""GPU parity of the DPT head's kernels against the oracle, through the C ABI:
+the 3x3 convolution (implicit GEMM on the matrix cores, strides 1 and 2, with
+and without bias, the ReLU prologue, epilogues), the 1x1 convolution (a
+matmul), the transposed convolution and the bilinear resampling, whole and
+split into parts; then a whole decoder at a small side against the oracle's
+composition of the same operations (reference.rs:194-244 for the residual unit
+and fusion layer) — the reference's crates/beatlm-bench/src/dpt.rs cases.
+
+Tolerance for f32 storage: |got - want| <= 1e-4 + 1e-4 |want|
+(reference.rs:22-24); for f16 storage, max abs error <= 2e-2 against the
+oracle on the same f16-rounded inputs.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from beatlm_amd import hip, ir
+from tests.blockdata import CHAIN as H_, CHAIN_OUT as Y, chain, max_abs_err
+
+pytestmark = pytest.mark.gpu
+
+F16_TOL = 2e-2
+
+
+def assert_close(got, want, what):
+    bad = oracle.first_mismatch(got, want)
+    assert bad is None, f"{what}: element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
+
+
+def run(ctx, g, values, parts=1, dtype=hip.F32, fusion=ir.FUSION_ON):
+    if dtype == hip.F16:
+        values = {k: v.astype(np.float16) for k, v in values.items()}
+    return ir.run_on_gpu(ctx, g, values, fusion, parts, True, dtype)[Y]
+
+
+def f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("h,w,cin,cout,stride,bias", [
+    (37, 37, 384, 64, 1, False),   # the neck's convolution at 518 pixels
+    (37, 37, 384, 384, 2, True),   # the last stage's stride-2 resampling
+    (19, 19, 64, 64, 1, True),
+    (20, 13, 48, 32, 1, True),
+    (5, 7, 3, 4, 1, True),         # channels not a whole vector: the element-wise gather
+    (9, 9, 8, 6, 2, False),
+    (1, 1, 32, 16, 1, True),
+])
+def test_conv3x3_matches_the_oracle(ctx, h, w, cin, cout, stride, bias):
+    x = oracle.uniform(11, h * w * cin, -2.0, 2.0)
+    wt = oracle.fan_in_weights(12, 9 * cin * cout, 9 * cin)
+    b = oracle.uniform(13, cout, -0.1, 0.1) if bias else None
+    vals = {0: x, 1: wt}
+    if bias:
+        vals[2] = b
+    o = ir.op(ir.OP_CONV3X3, [0, 1, 2 if bias else ir.NONE], [h, w, cin, cout, stride])
+    g = chain(vals, [o])
+    want = oracle.conv3x3(x, wt, b, h, w, cin, cout, stride)
+    for parts in (1, 3):
+        assert_close(run(ctx, g, vals, parts), want, f"conv3x3 {h}x{w}x{cin}->{cout} s{stride}, {parts} parts")
+    got16 = run(ctx, g, vals, 1, hip.F16)
+    want16 = oracle.conv3x3(f16(x), f16(wt), f16(b) if bias else None, h, w, cin, cout, stride)
+    assert max_abs_err(got16, want16) <= F16_TOL
+
+
+def test_the_relu_prologue_and_epilogues_of_a_residual_unit(ctx):
+    # x + conv2(relu(conv1(relu(x)))): the outer ReLU a prologue (x is read
+    # twice), the inner an epilogue, the add fused into conv2.
+    h, w, c = 19, 21, 64
+    x = oracle.uniform(21, h * w * c, -2.0, 2.0)
+    w1, w2 = oracle.fan_in_weights(22, 9 * c * c, 9 * c), oracle.fan_in_weights(23, 9 * c * c, 9 * c)
+    b1, b2 = oracle.uniform(24, c, -0.1, 0.1), oracle.uniform(25, c, -0.1, 0.1)
+    vals = {0: x, 1: w1, 2: b1, 3: w2, 4: b2}
+    n = h * w * c
+    ops = [ir.op(ir.OP_RELU, [0], [n]), ir.op(ir.OP_CONV3X3, [H_, 1, 2], [h, w, c, c, 1]),
+           ir.op(ir.OP_RELU, [H_ + 1], [n]), ir.op(ir.OP_CONV3X3, [H_ + 2, 3, 4], [h, w, c, c, 1]),
+           ir.op(ir.OP_ADD, [H_ + 3, 0], [n])]
+    g = chain(vals, ops)
+    names = g.lower(ir.FUSION_ON).names()
+    assert names == ["relu-conv2d3x3+relu", "conv2d3x3+add"]
+    first = oracle.conv3x3(oracle.relu(x), w1, b1, h, w, c, c)
+    want = oracle.add(oracle.conv3x3(oracle.relu(first), w2, b2, h, w, c, c), x)
+    for fusion in (ir.FUSION_ON, ir.FUSION_OFF):
+        for parts in (1, 4):
+            assert_close(run(ctx, g, vals, parts, fusion=fusion), want, f"residual unit fusion {fusion} parts {parts}")
+
+
+@pytest.mark.parametrize("h,w,cin,cout,f", [(37, 37, 48, 48, 4), (37, 37, 96, 96, 2), (3, 5, 7, 3, 2), (1, 2, 1, 1, 2)])
+def test_conv_transpose_matches_the_oracle(ctx, h, w, cin, cout, f):
+    x = oracle.uniform(31, h * w * cin, -2.0, 2.0)
+    wt = oracle.fan_in_weights(32, f * f * cin * cout, cin)
+    b = oracle.uniform(33, cout, -0.1, 0.1)
+    vals = {0: x, 1: wt, 2: b}
+    g = chain(vals, [ir.op(ir.OP_CONV_TRANSPOSE, [0, 1, 2], [h, w, cin, cout, f])])
+    want = oracle.conv_transpose(x, wt, b, h, w, cin, cout, f)
+    for parts in (1, 7):
+        assert_close(run(ctx, g, vals, parts), want, f"conv transpose {h}x{w}x{cin} f{f}, {parts} parts")
+    got16 = run(ctx, g, vals, 1, hip.F16)
+    assert max_abs_err(got16, oracle.conv_transpose(f16(x), f16(wt), f16(b), h, w, cin, cout, f)) <= F16_TOL
+
+
+@pytest.mark.parametrize("ih,iw,oh,ow,c", [(148, 148, 296, 296, 64), (19, 19, 37, 37, 64), (296, 296, 518, 518, 32),
+                                           (4, 5, 9, 7, 3), (5, 5, 1, 1, 2), (2, 2, 3, 3, 1)])
+def test_resize_bilinear_matches_the_oracle(ctx, ih, iw, oh, ow, c):
+    x = oracle.uniform(41, ih * iw * c, -2.0, 2.0)
+    vals = {0: x}
+    g = chain(vals, [ir.op(ir.OP_RESIZE_BILINEAR, [0], [ih, iw, oh, ow, c])])
+    want = oracle.resize_bilinear(x, ih, iw, oh, ow, c)
+    for parts in (1, 5):
+        assert_close(run(ctx, g, vals, parts), want, f"resize {ih}x{iw}->{oh}x{ow}x{c}, {parts} parts")
+    assert max_abs_err(run(ctx, g, vals, 1, hip.F16), oracle.resize_bilinear(f16(x), ih, iw, oh, ow, c)) <= F16_TOL
+
+
+def test_the_reference_known_answers_on_the_gpu(ctx):
+    # reference.rs tests: a transposed convolution writes one block per input
+    # pixel; aligned corners keep the corners and interpolate linearly.
+    vals = {0: np.array([10.0, -1.0], np.float32), 1: np.array([1.0, 2.0, 3.0, 4.0], np.float32),
+            2: np.array([0.5], np.float32)}
+    g = chain(vals, [ir.op(ir.OP_CONV_TRANSPOSE, [0, 1, 2], [1, 2, 1, 1, 2])])
+    assert np.array_equal(run(ctx, g, vals), [10.5, 20.5, -0.5, -1.5, 30.5, 40.5, -2.5, -3.5])
+    vals = {0: np.array([0.0, 2.0, 4.0, 6.0], np.float32)}
+    g = chain(vals, [ir.op(ir.OP_RESIZE_BILINEAR, [0], [2, 2, 3, 3, 1])])
+    assert np.array_equal(run(ctx, g, vals), [0, 1, 2, 2, 3, 4, 4, 5, 6])
+    vals = {0: np.ones(4, np.float32), 1: np.ones(9, np.float32), 2: np.array([0.5], np.float32)}
+    g = chain(vals, [ir.op(ir.OP_CONV3X3, [0, 1, 2], [2, 2, 1, 1, 1])])
+    assert np.array_equal(run(ctx, g, vals), [4.5] * 4)
+
+
+# ---- the whole decoder -------------------------------------------------------
+
+
+def fan_in_of(name, cfg):
+    """Fan-in of a decoder weight, for U(+-1/sqrt(fan_in)) draws that keep the
+    activations near unit scale through the 30-odd layers."""
+    F = cfg.fusion_hidden_size
+    parts = name.split(".")
+    if name.startswith("neck.reassemble_stage."):
+        i = int(parts[3])
+        ch = cfg.neck_hidden_sizes[i]
+        if parts[4] == "projection":
+            return cfg.hidden_size
+        return ch if cfg.reassemble[i][0] == "up" else 9 * ch
+    if name.startswith("neck.convs."):
+        return 9 * cfg.neck_hidden_sizes[int(parts[2])]
+    if name.startswith("neck.fusion_stage."):
+        return F if parts[4] == "projection" else 9 * F
+    return {"conv1": 9 * F, "conv2": 9 * (F // 2), "conv3": cfg.head_hidden_size}[parts[1]]
+
+
+def decoder_values(weights, cfg, seed=500):
+    """{id: values} and {name: values}: weights U(+-1/sqrt(fan_in)), biases
+    U(-0.1, 0.1)."""
+    by_id, by_name = {}, {}
+    for i, (tid, name, n) in enumerate(weights):
+        if name.endswith(".bias"):
+            v = oracle.uniform(seed + i, n, -0.1, 0.1)
+        else:
+            v = oracle.fan_in_weights(seed + i, n, fan_in_of(name, cfg))
+        by_id[tid] = by_name[name] = v
+    return by_id, by_name
+
+
+def oracle_decoder(cfg, side, features, w):
+    """The decoder's forward pass composed from the oracle's operations:
+    reference.rs:194-244 (residual unit, fusion layer) and
+    depth_anything_v2.rs:882-981 (the stages, the head)."""
+    grid, F = side // cfg.patch_size, cfg.fusion_hidden_size
+    stages = []
+    for i, feat in enumerate(features):
+        ch = cfg.neck_hidden_sizes[i]
+        pre = f"neck.reassemble_stage.layers.{i}"
+        m = oracle.conv1x1(feat, w[pre + ".projection.weight"], w[pre + ".projection.bias"], grid * grid,
+                           cfg.hidden_size, ch)
+        kind = cfg.reassemble[i]
+        if kind[0] == "up":
+            f = kind[1]
+            m = oracle.conv_transpose(m, w[pre + ".resize.weight"], w[pre + ".resize.bias"], grid, grid, ch, ch, f)
+            hw = (grid * f, grid * f)
+        elif kind[0] == "down":
+            m = oracle.conv3x3(m, w[pre + ".resize.weight"], w[pre + ".resize.bias"], grid, grid, ch, ch, kind[1])
+            hw = ((grid - 1) // kind[1] + 1,) * 2
+        else:
+            hw = (grid, grid)
+        stages.append((oracle.conv3x3(m, w[f"neck.convs.{i}.weight"], None, hw[0], hw[1], ch, F), hw))
+
+    def unit(x, name, hw):
+        a = oracle.conv3x3(oracle.relu(x), w[name + ".convolution1.weight"], w[name + ".convolution1.bias"], hw[0],
+                           hw[1], F, F)
+        b = oracle.conv3x3(oracle.relu(a), w[name + ".convolution2.weight"], w[name + ".convolution2.bias"], hw[0],
+                           hw[1], F, F)
+        return oracle.add(b, x)
+
+    fused = None
+    for layer, (stage, hw) in enumerate(reversed(stages)):
+        nxt = len(stages) - (layer + 2)
+        out = stages[nxt][1] if nxt >= 0 else (hw[0] * 2, hw[1] * 2)
+        name = f"neck.fusion_stage.layers.{layer}"
+        x = stage if fused is None else oracle.add(unit(stage, name + ".residual_layer1", hw), fused)
+        x = unit(x, name + ".residual_layer2", hw)
+        r = oracle.resize_bilinear(x, hw[0], hw[1], out[0], out[1], F)
+        fused = oracle.conv1x1(r, w[name + ".projection.weight"], w[name + ".projection.bias"], out[0] * out[1], F, F)
+        hw_out = out
+    full = grid * cfg.patch_size
+    first = oracle.conv3x3(fused, w["head.conv1.weight"], w["head.conv1.bias"], hw_out[0], hw_out[1], F, F // 2)
+    r = oracle.resize_bilinear(first, hw_out[0], hw_out[1], full, full, F // 2)
+    second = oracle.relu(oracle.conv3x3(r, w["head.conv2.weight"], w["head.conv2.bias"], full, full, F // 2,
+                                        cfg.head_hidden_size))
+    third = oracle.conv1x1(second, w["head.conv3.weight"], w["head.conv3.bias"], full * full, cfg.head_hidden_size, 1)
+    return oracle.relu(third)
+
+
+@pytest.mark.parametrize("side", [70, 98])
+def test_a_whole_decoder_matches_the_oracle(ctx, side):
+    cfg = ir.DepthConfig.small()
+    grid = side // cfg.patch_size
+    g = ir.Graph()
+    for i in range(4):
+        g.tensor(i, ir.INPUT, grid * grid * cfg.hidden_size)
+    depth, weights, _ = ir.depth_decoder(g, cfg, side, [0, 1, 2, 3], 10)
+    vals, named = decoder_values(weights, cfg)
+    features = [oracle.normal(900 + i, grid * grid * cfg.hidden_size) for i in range(4)]
+    vals.update(enumerate(features))
+    want = oracle_decoder(cfg, side, features, named)
+    assert float(np.max(want)) > 0.0  # the final ReLU leaves something to compare
+    for parts in (1, 2):
+        prep = ir.prepare(ctx, g, ir.FUSION_ON, parts)
+        for tid, v in vals.items():
+            prep.write(tid, v)
+        prep.run()
+        ctx.synchronize()
+        got = prep.read(depth)
+        assert got.size == side * side
+        assert_close(got, want, f"decoder at {side} pixels, {parts} parts")
