@@ -337,6 +337,24 @@ class DepthConfig:
     def small(cls) -> "DepthConfig":
         return cls()
 
+    def fan_in(self, name: str) -> int:
+        """Inputs summed into one output of a decoder weight named as
+        depth_decoder names it (a convolution's kh * kw * cin; a transposed
+        convolution's cin), for scaling random weights."""
+        parts = name.split(".")
+        fusion = self.fusion_hidden_size
+        if name.startswith("neck.reassemble_stage."):
+            i = int(parts[3])
+            ch = self.neck_hidden_sizes[i]
+            if parts[4] == "projection":
+                return self.hidden_size
+            return ch if self.reassemble[i][0] == "up" else 9 * ch
+        if name.startswith("neck.convs."):
+            return 9 * self.neck_hidden_sizes[int(parts[2])]
+        if name.startswith("neck.fusion_stage."):
+            return fusion if parts[4] == "projection" else 9 * fusion
+        return {"conv1": 9 * fusion, "conv2": 9 * (fusion // 2), "conv3": self.head_hidden_size}[parts[1]]
+
 
 class _Ids:
     """Tensor ids handed out in order, as the reference's Builder does

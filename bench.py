@@ -18,6 +18,11 @@ The same line carries `frame_loop`: the high-resolution encoder (ViT-S/14 at
 frames per second beside a render load spinning the GPU for 8 ms a frame,
 after calibration: slices per frame, the delivery latency k the calibrated
 costs call for, deliveries and misses (--frame-loop-frames 0 skips it).
+
+And `depth_model`: the whole Depth Anything V2 Small (the encoder with its four
+tapped feature maps and the DPT decoder) in f32 at the reference's five image
+sides, ms per run beside the reference's published per-run times
+(--depth-runs 0 skips it).
 """
 
 from __future__ import annotations
@@ -248,6 +253,68 @@ def layernorm_hbm(ctx, rows: int, width: int, repeats: int = 20) -> dict:
             "frac": round(gbs / PEAK_HBM_GBS, 4)}
 
 
+# Whole Depth Anything V2 Small per run on an M1 Pro (Metal, f32), the
+# reference's published figures (crates/beatlm-bench/src/main.rs:383-389).
+DEPTH_SIDES_MS = {518: 202.3, 434: 137.8, 350: 85.6, 266: 53.2, 182: 35.0}
+
+
+def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict:
+    """The whole model (12-layer encoder, four tapped feature maps, DPT
+    decoder) at each of the reference's five image sides: ms per run over
+    `runs` back-to-back runs, and at 518 pixels the summed per-launch time of
+    the encoder's and the decoder's kernels and the decoder's kernels by name."""
+    cfg = ir.DepthConfig.small()
+    np_dtype = np.float16 if dtype == hip.F16 else np.float32
+    out = {"workload": "Depth Anything V2 Small (ViT-S/14 encoder, taps 3/6/9/12, DPT decoder 48/96/192/384 -> "
+                       f"64 -> 32 -> 1), {'f16' if dtype == hip.F16 else 'f32'}, random weights, synthetic image",
+           "ms_per_run": {}, "reference_m1_pro_ms": {}}
+    for side in DEPTH_SIDES_MS:
+        grid = side // PATCH
+        g = ir.Graph()
+        enc = ir.vit_encoder(g, grid, PATCH, 3, cfg.hidden_size, cfg.num_heads, cfg.hidden_size * cfg.mlp_ratio,
+                             cfg.eps, cfg.out_indices, 0, ir.ACTIVATION)
+        encoder_ops = g.ops()
+        depth, weights, _ = ir.depth_decoder(g, cfg, side, enc.features, enc.next_id)
+        enc_cfg = dict(CONFIGS["vit-s-518"], grid=grid)
+        vals = synthetic_values(enc_cfg, enc.embed, enc.blocks, grid * grid + 1, np_dtype, seed=3000 + side)
+        rng = np.random.default_rng(side)
+        vals[enc.final_g] = (1 + 0.1 * rng.normal(0, 1, cfg.hidden_size)).astype(np_dtype)
+        vals[enc.final_b] = (0.1 * rng.normal(0, 1, cfg.hidden_size)).astype(np_dtype)
+        for tid, name, n in weights:
+            bound = 0.1 if name.endswith(".bias") else 1.0 / np.sqrt(cfg.fan_in(name))
+            vals[tid] = rng.uniform(-bound, bound, n).astype(np_dtype)
+        prep = ir.prepare(ctx, g, dtype=dtype)
+        for tid, v in vals.items():
+            prep.write(tid, v)
+        prep.run()
+        ctx.synchronize()
+        allocs = ctx.allocations()
+        t0 = time.perf_counter()
+        for _ in range(runs):
+            prep.run()
+        ctx.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / runs
+        assert ctx.allocations() == allocs, "the model's runs allocated device memory"
+        d = prep.read(depth).astype(np.float32)
+        assert d.size == side * side and np.isfinite(d).all(), "non-finite depth"
+        out["ms_per_run"][str(side)] = round(ms, 3)
+        out["reference_m1_pro_ms"][str(side)] = DEPTH_SIDES_MS[side]
+        if side == 518:
+            n = len(prep.kernels)
+            us = [prep.kernels.time(k, repeats) for k in range(n)]
+            dec = [k for k in range(n) if prep.program.kernel(k).first_op >= encoder_ops]
+            by_name: dict[str, float] = {}
+            for k in dec:
+                by_name[prep.program.name(k)] = by_name.get(prep.program.name(k), 0.0) + us[k]
+            out["kernels_at_518"] = len(prep.kernels)
+            out["encoder_kernel_ms_at_518"] = round(sum(us[k] for k in range(n) if k not in dec) / 1e3, 3)
+            out["decoder_kernel_ms_at_518"] = round(sum(us[k] for k in dec) / 1e3, 3)
+            out["decoder_us_by_kernel_at_518"] = {k: round(v, 1) for k, v in sorted(by_name.items(), key=lambda x: -x[1])}
+            out["plan_bytes_at_518"] = prep.plan.total_bytes()
+        del prep
+    return out
+
+
 def cpu_baseline(cfg, tokens, threads):
     """The reference's WGSL kernels' arithmetic (oracle, f32, same summation
     order) for ONE block of this workload on the host cores: 1 warm-up, median
@@ -288,6 +355,7 @@ def main() -> int:
     ap.add_argument("--kernel-repeats", type=int, default=20)
     ap.add_argument("--pmc-summary", metavar="DIR", help="write the counter summary of a profile directory and exit")
     ap.add_argument("--frame-loop-frames", type=int, default=120)
+    ap.add_argument("--depth-runs", type=int, default=20, help="runs of the whole depth model per side (0 skips it)")
     ap.add_argument("--layernorm-rows", type=int, default=262144)
     ap.add_argument("--render-us", type=int, default=8000)
     ap.add_argument("--max-dispatch-us", type=int, default=frameloop.DEFAULT_MAX_DISPATCH_US)
@@ -433,6 +501,9 @@ def main() -> int:
         loop["workload"] = (f"vit-s-1036: patch embed + {hi['blocks']} pre-LN ViT blocks, {tokens5} tokens, "
                             f"width 384, 6 heads x 64, f16, as " + loop["workload"])
         result["frame_loop"] = loop
+
+    if args.depth_runs > 0:
+        result["depth_model"] = depth_model_runs(ctx, args.depth_runs, args.kernel_repeats)
 
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)

@@ -130,24 +130,6 @@ def test_the_reference_known_answers_on_the_gpu(ctx):
 # ---- the whole decoder -------------------------------------------------------
 
 
-def fan_in_of(name, cfg):
-    """Fan-in of a decoder weight, for U(+-1/sqrt(fan_in)) draws that keep the
-    activations near unit scale through the 30-odd layers."""
-    F = cfg.fusion_hidden_size
-    parts = name.split(".")
-    if name.startswith("neck.reassemble_stage."):
-        i = int(parts[3])
-        ch = cfg.neck_hidden_sizes[i]
-        if parts[4] == "projection":
-            return cfg.hidden_size
-        return ch if cfg.reassemble[i][0] == "up" else 9 * ch
-    if name.startswith("neck.convs."):
-        return 9 * cfg.neck_hidden_sizes[int(parts[2])]
-    if name.startswith("neck.fusion_stage."):
-        return F if parts[4] == "projection" else 9 * F
-    return {"conv1": 9 * F, "conv2": 9 * (F // 2), "conv3": cfg.head_hidden_size}[parts[1]]
-
-
 def decoder_values(weights, cfg, seed=500):
     """{id: values} and {name: values}: weights U(+-1/sqrt(fan_in)), biases
     U(-0.1, 0.1)."""
@@ -156,7 +138,7 @@ def decoder_values(weights, cfg, seed=500):
         if name.endswith(".bias"):
             v = oracle.uniform(seed + i, n, -0.1, 0.1)
         else:
-            v = oracle.fan_in_weights(seed + i, n, fan_in_of(name, cfg))
+            v = oracle.fan_in_weights(seed + i, n, cfg.fan_in(name))
         by_id[tid] = by_name[name] = v
     return by_id, by_name
 
@@ -232,3 +214,65 @@ def test_a_whole_decoder_matches_the_oracle(ctx, side):
         got = prep.read(depth)
         assert got.size == side * side
         assert_close(got, want, f"decoder at {side} pixels, {parts} parts")
+
+
+# ---- the whole model ---------------------------------------------------------
+
+
+def encoder_values(enc, cfg, grid, seed=60):
+    """Image U[0,1], patch weights U(+-1/sqrt(588)), class token, positions and
+    the final LayerNorm as the encoder test draws them, block weights by the
+    reference's scheme (vit.rs:206-231)."""
+    from tests.blockdata import block_weights
+
+    d, t, p = cfg.hidden_size, grid * grid + 1, cfg.patch_size
+    e = enc.embed
+    vals = {e.image: oracle.uniform(seed, (grid * p) ** 2 * 3, 0.0, 1.0),
+            e.patch_w: oracle.fan_in_weights(seed + 1, p * p * 3 * d, p * p * 3),
+            e.patch_b: oracle.uniform(seed + 2, d, -0.1, 0.1), e.cls: oracle.uniform(seed + 3, d, -1.0, 1.0),
+            e.pos: oracle.uniform(seed + 4, t * d, -0.5, 0.5), enc.final_g: oracle.uniform(seed + 5, d, 0.8, 1.2),
+            enc.final_b: oracle.uniform(seed + 6, d, -0.1, 0.1)}
+    for i, ids in enumerate(enc.blocks):
+        w = block_weights(d, d * cfg.mlp_ratio, 100 + 20 * i, "reference")
+        for name in ir.BLOCK_WEIGHTS:
+            vals[getattr(ids, name)] = w[name]
+    return vals
+
+
+def oracle_encoder(enc, cfg, grid, f32):
+    d, h, t = cfg.hidden_size, cfg.num_heads, grid * grid + 1
+    e = enc.embed
+    x = oracle.add(oracle.prepend_token(f32[e.cls], oracle.patch_embed(f32[e.image], f32[e.patch_w], f32[e.patch_b],
+                                                                          grid, grid, cfg.patch_size, 3, d),
+                                        grid * grid, d), f32[e.pos])
+    features = []
+    for i, ids in enumerate(enc.blocks):
+        w = {name: f32[getattr(ids, name)] for name in ir.BLOCK_WEIGHTS}
+        x = oracle.vit_block(x, w, t, h, d // h, d * cfg.mlp_ratio, cfg.eps)
+        if i + 1 in cfg.out_indices:
+            features.append(oracle.layernorm(x, f32[enc.final_g], f32[enc.final_b], t, d, cfg.eps)[d:])
+    return features
+
+
+@pytest.mark.parametrize("dtype", [hip.F32, hip.F16])
+def test_the_whole_model_matches_the_oracle(ctx, dtype):
+    """model() (depth_anything_v2.rs:984-995) at 70 pixels: the 12-layer
+    encoder, its four tapped feature maps as activations, and the decoder."""
+    cfg = ir.DepthConfig.small()
+    side = 70
+    grid = side // cfg.patch_size
+    g = ir.Graph()
+    m = ir.depth_model(g, cfg, side)
+    vals = encoder_values(m.encoder, cfg, grid)
+    dec, named = decoder_values(m.decoder_weights, cfg)
+    vals.update(dec)
+    if dtype == hip.F16:
+        vals = {k: f16(v) for k, v in vals.items()}
+        named = {n: vals[tid] for tid, n, _ in m.decoder_weights}
+    want = oracle_decoder(cfg, side, oracle_encoder(m.encoder, cfg, grid, vals), named)
+    got = ir.run_on_gpu(ctx, g, vals, dtype=dtype)
+    assert list(got) == [m.depth]
+    if dtype == hip.F16:
+        assert max_abs_err(got[m.depth], want) <= F16_TOL
+    else:
+        assert_close(got[m.depth], want, "depth at 70 pixels")
