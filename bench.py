@@ -129,6 +129,10 @@ def kernel_flops(info) -> float:
         return 4.0 * rows * d[0] * d[1] * d[2]
     if info.main == hip.MAIN_PATCH_EMBED:
         return 2.0 * rows * d[2] * d[2] * d[3] * d[4]
+    if info.main == hip.MAIN_CONV3X3:  # rows are output pixels
+        return 2.0 * rows * 9 * d[2] * d[3]
+    if info.main == hip.MAIN_CONV_TRANSPOSE:  # rows are output pixels, each cin products per channel
+        return 2.0 * rows * d[2] * d[3]
     return 0.0
 
 
