@@ -280,7 +280,7 @@ extern "C" int bl_arenas_device_ptr(bl_arenas *a, uint32_t arena, uint64_t offse
 
 namespace {
 
-enum class Family { LAYER_NORM, GEMM, GATHER, SOFTMAX, FLASH, ELEMENT, DPT };
+enum class Family { LAYER_NORM, GEMM, GATHER, SOFTMAX, FLASH, ELEMENT, DPT, GEMV };
 
 struct Launch {
     Family family;
@@ -298,6 +298,7 @@ struct Launch {
     ElementArgs el;
     Dpt dpt = Dpt::RESIZE;
     DptArgs dp;
+    GemvArgs gv;
 };
 
 struct Kernel {
@@ -483,6 +484,7 @@ struct bl_kernels {
     std::vector<Kernel> kernels;
     uint32_t sets = 1;
     void *scratch = nullptr;
+    float *partials = nullptr;  // split-k GEMMs' partial sums, shared as the attention scratch is
     std::vector<Pack> packs;
     void *pack_buffer = nullptr;
     std::vector<RangeGraph> graphs;
@@ -601,6 +603,8 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     ks->sets = n_sets;
     uint64_t scratch_bytes = 0;
     std::vector<std::pair<size_t, size_t>> flash_users;  // (kernel, set) whose FlashArgs need scratch
+    uint64_t partial_bytes = 0;
+    std::vector<std::pair<size_t, size_t>> split_users;  // (kernel, set) of split-k GEMMs
 
     auto bad = [&](int code, const char *fmt, auto... args) {
         delete ks;
@@ -731,6 +735,14 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
             case BL_MAIN_MATMUL:
             case BL_MAIN_PATCH_EMBED:
             case BL_MAIN_CONV3X3: {
+                // At most 4 output columns (the head's 1x1 convolution to one
+                // channel): a 64-wide MFMA tile would be all padding.
+                if (s.main == BL_MAIN_MATMUL && d[2] <= 4 && d[1] % 4 == 0 && !getenv("BL_NO_GEMV")) {
+                    L.family = Family::GEMV;
+                    L.gv = GemvArgs{rd(0), rd(1), d[3] ? rd(2) : nullptr, out_ptr, d[1], d[2], pt.start, pt.end, epi};
+                    variant = "valu-gemv";
+                    break;
+                }
                 L.family = Family::GEMM;
                 const bool patch = s.main == BL_MAIN_PATCH_EMBED, conv = s.main == BL_MAIN_CONV3X3;
                 const uint32_t conv_oh = conv ? (d[0] - 1) / d[4] + 1 : 0, conv_ow = conv ? (d[1] - 1) / d[4] + 1 : 0;
@@ -750,7 +762,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 ga.row0 = pt.start;
                 ga.row1 = pt.end;
                 ga.load = patch ? 2 : conv ? 3 : 0;
-                ga.pipeline = getenv("BL_GEMM_NO_PIPELINE") ? 0 : 1;
+                ga.pipeline = getenv("BL_GEMM_NO_PIPELINE") || (conv && getenv("BL_CONV_NO_PIPELINE")) ? 0 : 1;
                 if (patch) {
                     ga.p0 = d[1];
                     ga.p1 = d[2];
@@ -832,12 +844,43 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 if (const char *force = getenv("BL_GEMM_STAGES")) ga.stages = (uint32_t)atoi(force);
                 ga.kslices = 1;
                 if (const char *force = getenv("BL_GEMM_KSLICES")) ga.kslices = (uint32_t)atoi(force);
+                // A 3x3 convolution with fewer tiles than CUs (the decoder's deep,
+                // narrow stages: 6 tiles and 108 k-steps at 19 x 19 x 384 -> 64)
+                // is bound by its serial k-loop: split k over up to two
+                // workgroups per CU, at least two k-steps each.
+                // A convolution to 32 channels or fewer over many pixels (the
+                // head's): 128 x 32 tiles, so B is not half padding and A is
+                // read by a quarter as many workgroups.
+                // Otherwise 32 x 64: a convolution's window loads wait longer than
+                // a plain row's, and the smaller tile's extra workgroups hide it
+                // (148 x 148 x 64 -> 64: 19.8 us against 24.6 with 64 x 64).
+                if (conv && !getenv("BL_GEMM_TILE"))
+                    chosen = gn <= 32 && wgs_of(TILE_128x32) >= ctx->compute_units ? TILE_128x32 : TILE_32x64;
+                ga.ksplit = 1;
+                if (conv && !getenv("BL_CONV_NO_SPLIT_K")) {
+                    const uint64_t wgs = wgs_of(chosen);
+                    const uint32_t steps = ga.k_pad / 32;
+                    if (wgs < ctx->compute_units && steps >= 4) {
+                        uint64_t want = std::min<uint64_t>(steps / 2, (2ull * ctx->compute_units + wgs - 1) / wgs);
+                        if (const char *force = getenv("BL_CONV_SPLIT_K")) want = (uint64_t)atoi(force);
+                        if (want >= 2) {
+                            // No empty split: ceil(steps / per) runs of per steps.
+                            const uint32_t per = (uint32_t)((steps + want - 1) / want);
+                            ga.ksplit = (steps + per - 1) / per;
+                        }
+                    }
+                    if (ga.ksplit > 1) {
+                        partial_bytes = std::max<uint64_t>(partial_bytes, (uint64_t)ga.ksplit * rows * gn * sizeof(float));
+                        split_users.push_back({ki, si});
+                    }
+                }
                 L.gemm = ga;
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
                           " " + std::to_string(gemm_tile_rows(chosen)) + "x" +
                           std::to_string(gemm_tile_cols(chosen)) +
-                          (ga.kgroups > 1 ? " k" + std::to_string(ga.kgroups) : std::string());
+                          (ga.kgroups > 1 && !conv ? " k" + std::to_string(ga.kgroups) : std::string()) +
+                          (ga.ksplit > 1 ? " splitk" + std::to_string(ga.ksplit) : std::string());
                 break;
             }
             case BL_MAIN_ATTENTION_SCORES:
@@ -950,6 +993,13 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
             for (Launch &L : k.per_set)
                 if (L.pack >= 0) L.gemm.b = (char *)ks->pack_buffer + ks->packs[L.pack].dst_offset;
     }
+    if (partial_bytes) {
+        // Split-k GEMMs run one after another on the stream: one buffer serves
+        // them all, every element written by its split before the reduce reads it.
+        ks->partials = (float *)bl_device_alloc(ctx, partial_bytes);
+        if (!ks->partials) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of split-k partial sums", (unsigned long long)partial_bytes);
+        for (auto [ki, si] : split_users) ks->kernels[ki].per_set[si].gemm.partials = ks->partials;
+    }
     if (scratch_bytes) {
         ks->scratch = bl_device_alloc(ctx, scratch_bytes);
         if (!ks->scratch) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
@@ -1005,6 +1055,7 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
     hipStreamSynchronize(k->ctx->stream);
     for (RangeGraph &g : k->graphs) hipGraphExecDestroy(g.exec);
     if (k->scratch) hipFree(k->scratch);
+    if (k->partials) hipFree(k->partials);
     if (k->pack_buffer) hipFree(k->pack_buffer);
     bl_ctx *ctx = k->ctx;
     delete k;
@@ -1030,12 +1081,16 @@ static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
 static hipError_t launch(const Launch &L, hipStream_t s) {
     switch (L.family) {
     case Family::LAYER_NORM: return launch_layernorm(L.ln, L.f16, s);
-    case Family::GEMM: return launch_gemm(L.gemm, L.math, L.tile, s);
+    case Family::GEMM: {
+        const hipError_t e = launch_gemm(L.gemm, L.math, L.tile, s);
+        return e == hipSuccess && L.gemm.ksplit > 1 ? launch_gemm_reduce(L.gemm, L.f16, s) : e;
+    }
     case Family::GATHER: return launch_gather(L.ga, L.gather, L.f16, s);
     case Family::SOFTMAX: return launch_softmax(L.sm, L.f16, s);
     case Family::FLASH: return launch_flash(L.fl, L.math, s);
     case Family::ELEMENT: return launch_element(L.el, L.element, L.f16, s);
     case Family::DPT: return launch_dpt(L.dp, L.dpt, L.f16, s);
+    case Family::GEMV: return launch_gemv(L.gv, L.f16, s);
     }
     return hipErrorInvalidValue;
 }

@@ -350,28 +350,54 @@ __global__ __launch_bounds__(256) void element_kernel(ElementArgs a) {
 }
 
 // ------------------------------------------------------------------------
-// The DPT head's gathers, one output element per invocation.
+// The DPT head's gathers, V consecutive channels of one output pixel per
+// invocation (V = 4 when the channel count is a multiple of 4, else 1).
 //
 // Transposed convolution, kernel = stride = f (ConvTranspose2d,
 // kernel.rs:547-597): output pixel (Y, X) lies in the f x f block of input
 // pixel (Y / f, X / f) at tap (Y % f, X % f), and no other input pixel reaches
 // it, so each output element is the bias plus one dot product over the input
-// channels (the reference's own kernel gathers the same way). Lanes of a wave
-// take consecutive output channels: the input pixel is shared, the HWIO
-// weight reads are contiguous.
+// channels (the reference's own kernel gathers the same way). An input value
+// serves the V channels; the HWIO weights of V channels are one vector load.
 //
 // Bilinear resampling with aligned corners (ResizeBilinear,
 // kernel.rs:599-631): positions as PyTorch's interpolate computes them in f32,
 // ratio * index, the floor and the next index clamped to the last row or
-// column, weights 1 - l and l.
+// column, weights 1 - l and l; each corner one vector load.
 // ------------------------------------------------------------------------
-template <Dpt K, typename T>
+template <typename T, int V> struct VecOf { typedef T type __attribute__((ext_vector_type(V))); };
+template <typename T> struct VecOf<T, 1> { typedef T type; };
+
+template <typename T, int V>
+__device__ __forceinline__ void load_vec(const T *p, float (&v)[V]) {
+    if constexpr (V == 1) {
+        v[0] = to_f32(*p);
+    } else {
+        const typename VecOf<T, V>::type x = *(const typename VecOf<T, V>::type *)p;
+#pragma unroll
+        for (int e = 0; e < V; e++) v[e] = to_f32(x[e]);
+    }
+}
+template <typename T, int V>
+__device__ __forceinline__ void store_vec(T *p, const float (&v)[V]) {
+    if constexpr (V == 1) {
+        *p = from_f32<T>(v[0]);
+    } else {
+        typename VecOf<T, V>::type x;
+#pragma unroll
+        for (int e = 0; e < V; e++) x[e] = from_f32<T>(v[e]);
+        *(typename VecOf<T, V>::type *)p = x;
+    }
+}
+
+template <Dpt K, typename T, int V>
 __global__ __launch_bounds__(256) void dpt_kernel(DptArgs a) {
     const T *X = (const T *)a.x;
     T *Y = (T *)a.y;
-    for (uint64_t i = a.start + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < a.end;
-         i += (uint64_t)gridDim.x * 256) {
-        float v;
+    const uint64_t groups = (a.end - a.start) / V;
+    for (uint64_t gi = (uint64_t)blockIdx.x * 256 + threadIdx.x; gi < groups; gi += (uint64_t)gridDim.x * 256) {
+        const uint64_t i = a.start + gi * V;
+        float v[V];
         if constexpr (K == Dpt::CONV_TRANSPOSE) {
             const uint32_t w = a.d[1], cin = a.d[2], cout = a.d[3], f = a.d[4];
             const uint64_t pixel = i / cout;
@@ -381,9 +407,35 @@ __global__ __launch_bounds__(256) void dpt_kernel(DptArgs a) {
             const uint32_t y = oy / f, ky = oy % f, x = ox / f, kx = ox % f;
             const T *in = X + ((uint64_t)y * w + x) * cin;
             const T *wt = (const T *)a.w + ((uint64_t)(ky * f + kx) * cin) * cout + co;
-            float acc = 0.0f;
-            for (uint32_t ci = 0; ci < cin; ci++) acc += to_f32(in[ci]) * to_f32(wt[(uint64_t)ci * cout]);
-            v = acc + (a.d[5] ? to_f32(((const T *)a.bias)[co]) : 0.0f);
+            float acc[V];
+#pragma unroll
+            for (int e = 0; e < V; e++) acc[e] = 0.0f;
+            uint32_t ci = 0;
+            if (cin % 4 == 0) {
+                // Input channels four at a time (one vector load), summed in order.
+                for (; ci < cin; ci += 4) {
+                    float xv[4];
+                    load_vec<T, 4>(in + ci, xv);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float wv[V];
+                        load_vec<T, V>(wt + (uint64_t)(ci + q) * cout, wv);
+#pragma unroll
+                        for (int e = 0; e < V; e++) acc[e] += xv[q] * wv[e];
+                    }
+                }
+            }
+            for (; ci < cin; ci++) {
+                const float xv = to_f32(in[ci]);
+                float wv[V];
+                load_vec<T, V>(wt + (uint64_t)ci * cout, wv);
+#pragma unroll
+                for (int e = 0; e < V; e++) acc[e] += xv * wv[e];
+            }
+            float b[V];
+            if (a.d[5]) load_vec<T, V>((const T *)a.bias + co, b);
+#pragma unroll
+            for (int e = 0; e < V; e++) v[e] = acc[e] + (a.d[5] ? b[e] : 0.0f);
         } else {
             const uint32_t ih = a.d[0], iw = a.d[1], ow = a.d[3], c = a.d[4];
             const uint64_t pixel = i / c;
@@ -393,12 +445,93 @@ __global__ __launch_bounds__(256) void dpt_kernel(DptArgs a) {
             const uint32_t y0 = min((uint32_t)py, ih - 1), x0 = min((uint32_t)px, iw - 1);
             const uint32_t y1 = min(y0 + 1, ih - 1), x1 = min(x0 + 1, iw - 1);
             const float ly = py - (float)y0, lx = px - (float)x0;
-            auto at = [&](uint32_t yy, uint32_t xx) { return to_f32(X[((uint64_t)yy * iw + xx) * c + ch]); };
-            const float top = (1.0f - lx) * at(y0, x0) + lx * at(y0, x1);
-            const float bottom = (1.0f - lx) * at(y1, x0) + lx * at(y1, x1);
-            v = (1.0f - ly) * top + ly * bottom;
+            float p00[V], p01[V], p10[V], p11[V];
+            load_vec<T, V>(X + ((uint64_t)y0 * iw + x0) * c + ch, p00);
+            load_vec<T, V>(X + ((uint64_t)y0 * iw + x1) * c + ch, p01);
+            load_vec<T, V>(X + ((uint64_t)y1 * iw + x0) * c + ch, p10);
+            load_vec<T, V>(X + ((uint64_t)y1 * iw + x1) * c + ch, p11);
+#pragma unroll
+            for (int e = 0; e < V; e++) {
+                const float top = (1.0f - lx) * p00[e] + lx * p01[e];
+                const float bottom = (1.0f - lx) * p10[e] + lx * p11[e];
+                v[e] = (1.0f - ly) * top + ly * bottom;
+            }
         }
-        Y[i] = from_f32<T>(apply_epilogue<T>(a.epi, v, i));
+#pragma unroll
+        for (int e = 0; e < V; e++) v[e] = apply_epilogue<T>(a.epi, v[e], i + e);
+        store_vec<T, V>(Y + i, v);
+    }
+}
+
+// ------------------------------------------------------------------------
+// Products with at most 4 output columns, on the vector ALUs: 8 lanes per row
+// read its k as 16-byte runs (a row of 32 f32 is one coalesced 128-byte
+// read), each lane summing its chunks k = 4 (lane % 8) + 32 j in order; the
+// 8 partial sums meet by shuffles, then bias and epilogue as the GEMM's.
+// ------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    const uint32_t sub = threadIdx.x & 7, N = a.n, K = a.k;
+    const T *B = (const T *)a.b;
+    for (uint64_t row = a.row0 + ((uint64_t)blockIdx.x * 256 + threadIdx.x) / 8; row < a.row1;
+         row += (uint64_t)gridDim.x * 32) {
+        const T *x = (const T *)a.a + row * K;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t k = 4 * sub; k < K; k += 32) {
+            float xv[4];
+            load_vec<T, 4>(x + k, xv);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if ((uint32_t)c < N) acc[c] += xv[e] * to_f32(B[(uint64_t)(k + e) * N + c]);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            acc[c] += __shfl_xor(acc[c], 1, 8);
+            acc[c] += __shfl_xor(acc[c], 2, 8);
+            acc[c] += __shfl_xor(acc[c], 4, 8);
+        }
+        if (sub == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                if ((uint32_t)c < N) {
+                    const uint64_t idx = row * N + c;
+                    const float v = acc[c] + (a.bias ? to_f32(((const T *)a.bias)[c]) : 0.0f);
+                    ((T *)a.c)[idx] = from_f32<T>(apply_epilogue<T>(a.epi, v, idx));
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------
+// The second pass of a split-k GEMM: output element i of the part (row
+// row0 + i / n, column i % n) is the sum of its ksplit partial sums in split
+// order, plus the bias, through the epilogue steps in order — what the
+// unsplit kernel's store does with one sum.
+// ------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a) {
+    const uint32_t N = a.n;
+    const uint64_t total = (uint64_t)(a.row1 - a.row0) * N;
+    const T *bias = (const T *)a.bias;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256) {
+        // Four partials in flight at a time, added in split order.
+        const float *p = a.partials + i;
+        float v = 0.0f;
+        uint32_t z = 0;
+        for (; z + 4 <= a.ksplit; z += 4) {
+            const float p0 = p[z * total], p1 = p[(z + 1) * total], p2 = p[(z + 2) * total], p3 = p[(z + 3) * total];
+            v += p0;
+            v += p1;
+            v += p2;
+            v += p3;
+        }
+        for (; z < a.ksplit; z++) v += p[z * total];
+        if (bias) v += to_f32(bias[i % N]);
+        const uint64_t idx = (uint64_t)a.row0 * N + i;
+        store_elem<T>((T *)a.c, idx, apply_epilogue<T>(a.epi, v, idx), a.c_planes);
     }
 }
 
@@ -457,15 +590,41 @@ hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStrea
 
 hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s) {
     if (a.end <= a.start) return hipSuccess;
-    uint64_t blocks = (a.end - a.start + 255) / 256;
+    // Channels per pixel: the part's range is whole pixels of them.
+    const uint32_t channels = k == Dpt::CONV_TRANSPOSE ? a.d[3] : a.d[4];
+    const int v = channels % 4 == 0 ? 4 : 1;
+    uint64_t blocks = ((a.end - a.start) / v + 255) / 256;
     if (blocks > 65535) blocks = 65535;
     dim3 grid((uint32_t)blocks);
-#define BL_DPT(K)                                                                      \
-    if (f16) hipLaunchKernelGGL((dpt_kernel<K, _Float16>), grid, dim3(256), 0, s, a); \
-    else hipLaunchKernelGGL((dpt_kernel<K, float>), grid, dim3(256), 0, s, a);
-    if (k == Dpt::CONV_TRANSPOSE) { BL_DPT(Dpt::CONV_TRANSPOSE) }
-    else { BL_DPT(Dpt::RESIZE) }
+#define BL_DPT(K, V)                                                                       \
+    if (f16) hipLaunchKernelGGL((dpt_kernel<K, _Float16, V>), grid, dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((dpt_kernel<K, float, V>), grid, dim3(256), 0, s, a);
+    if (k == Dpt::CONV_TRANSPOSE) {
+        if (v == 4) { BL_DPT(Dpt::CONV_TRANSPOSE, 4) } else { BL_DPT(Dpt::CONV_TRANSPOSE, 1) }
+    } else {
+        if (v == 4) { BL_DPT(Dpt::RESIZE, 4) } else { BL_DPT(Dpt::RESIZE, 1) }
+    }
 #undef BL_DPT
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(const GemvArgs &a, bool f16, hipStream_t s) {
+    if (a.row1 <= a.row0) return hipSuccess;
+    if (a.n == 0 || a.n > 4 || a.k % 4 != 0) return hipErrorInvalidValue;
+    uint64_t blocks = ((uint64_t)(a.row1 - a.row0) + 31) / 32;
+    if (blocks > 65535) blocks = 65535;
+    if (f16) hipLaunchKernelGGL(gemv_kernel<_Float16>, dim3((uint32_t)blocks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(gemv_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_reduce(const GemmArgs &a, bool f16, hipStream_t s) {
+    const uint64_t total = (uint64_t)(a.row1 - a.row0) * a.n;
+    if (total == 0) return hipSuccess;
+    uint64_t blocks = (total + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (f16) hipLaunchKernelGGL(gemm_reduce_kernel<_Float16>, dim3((uint32_t)blocks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(gemm_reduce_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -52,6 +52,13 @@ struct GemmArgs {
     uint32_t kslices;     // pipelined kernel: 32-wide k-slices per ring stage (1 or 2)
     uint32_t p0, p1, p2, p3;  // patches: grid_w, patch, cin, image width; conv3x3: height, width, cin, stride
     uint32_t p4, p5;          // conv3x3: output width, ReLU prologue (1) or none (0)
+    // Split k (the non-pipelined kernel, gathered A only): ksplit > 1
+    // workgroups per tile (blockIdx.y) each multiply a contiguous run of the
+    // k-steps and write their raw sums to partials [ksplit][row1 - row0][n];
+    // gemm_reduce_kernel then adds them in split order, adds the bias and
+    // runs the epilogue.
+    uint32_t ksplit;
+    float *partials;
     EpilogueArgs epi;
     // The QKV projection of a flash attention kernel also writes that
     // kernel's K [planes][H][t_pad][64] and Vt [planes][H][64][t_pad]
@@ -63,6 +70,8 @@ struct GemmArgs {
     // apart (0: f32).
     uint64_t a_planes, c_planes;
 };
+
+hipError_t launch_gemm_reduce(const GemmArgs &a, bool f16, hipStream_t s);
 
 // B [k][n] -> the GEMM's packed operand (transposed, padded, converted).
 struct PackArgs {
@@ -145,9 +154,20 @@ struct ElementArgs {
     EpilogueArgs epi;
 };
 
+// A product with at most 4 output columns (the depth head's 1x1 convolution
+// to one channel): rows [row0, row1) of C [m][n] = A [m][k] B [k][n] + bias,
+// then the epilogue; B as the plan holds it, k a multiple of 4.
+struct GemvArgs {
+    const void *a, *b, *bias;
+    void *c;
+    uint32_t k, n, row0, row1;
+    EpilogueArgs epi;
+};
+
 // ---- launchers (one per kernel family), defined with their kernels ----
 
 hipError_t launch_layernorm(const LayerNormArgs &a, bool f16, hipStream_t s);
+hipError_t launch_gemv(const GemvArgs &a, bool f16, hipStream_t s);
 hipError_t launch_gemm_f32(const GemmArgs &a, int tile, hipStream_t s);
 hipError_t launch_gemm_split(const GemmArgs &a, int tile, hipStream_t s);
 hipError_t launch_gemm_f16(const GemmArgs &a, int tile, hipStream_t s);
@@ -177,9 +197,9 @@ hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
 hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s);
 
 // GEMM tile shapes the dispatcher can pick from: BM x BN.
-enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_COUNT = 4 };
-inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128}; return r[t]; }
-inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64}; return c[t]; }
+enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_128x32 = 4, TILE_COUNT = 5 };
+inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128}; return r[t]; }
+inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64, 32}; return c[t]; }
 // K and N of a packed B are padded to these.
 constexpr uint32_t PACK_K = 32, PACK_N = 128;
 

@@ -46,6 +46,8 @@ def f16(a):
     (5, 7, 3, 4, 1, True),         # channels not a whole vector: the element-wise gather
     (9, 9, 8, 6, 2, False),
     (1, 1, 32, 16, 1, True),
+    (184, 184, 32, 32, 1, True),   # 32 channels over many pixels: the 128 x 32 tile
+    (181, 181, 16, 20, 1, False),  # ... with ragged output channels
 ])
 def test_conv3x3_matches_the_oracle(ctx, h, w, cin, cout, stride, bias):
     x = oracle.uniform(11, h * w * cin, -2.0, 2.0)
