@@ -46,6 +46,7 @@ SOURCES = [
     "cost.cpp",
     "schedule.cpp",
     "step.cpp",
+    "load.cpp",
 ]
 
 

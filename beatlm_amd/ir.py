@@ -332,6 +332,7 @@ class DepthConfig:
     fusion_hidden_size: int = 64
     head_hidden_size: int = 32
     eps: float = 1e-6
+    mask_token: bool = True  # the checkpoint holds backbone.embeddings.mask_token (unused by inference)
 
     @classmethod
     def small(cls) -> "DepthConfig":

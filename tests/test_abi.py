@@ -1,6 +1,6 @@
 """The C ABI as a drop-in boundary: the library loads without a GPU, exports
-every function include/beatlm_hip.h, include/beatlm_ir.h and
-include/beatlm_schedule.h declare, and the
+every function include/beatlm_hip.h, include/beatlm_ir.h,
+include/beatlm_schedule.h and include/beatlm_load.h declare, and the
 structs the host bindings pass have the C layout (checked against gcc
 compiling the headers). CPU only; no compute call."""
 
@@ -11,21 +11,22 @@ import subprocess
 
 import pytest
 
-from beatlm_amd import hip, ir, schedule
+from beatlm_amd import hip, ir, load, schedule
 
 ROOT = pathlib.Path(__file__).resolve().parent.parent
-HEADERS = [ROOT / "include" / "beatlm_hip.h", ROOT / "include" / "beatlm_ir.h", ROOT / "include" / "beatlm_schedule.h"]
+HEADERS = [ROOT / "include" / "beatlm_hip.h", ROOT / "include" / "beatlm_ir.h", ROOT / "include" / "beatlm_schedule.h",
+           ROOT / "include" / "beatlm_load.h"]
 
 
 def declared_functions(path):
     text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(bl[is]?_[a-z0-9_]+)\s*\(", text)) - {"bl_timer_stats_t"})
+    return sorted(set(re.findall(r"\b(bl[isf]?_[a-z0-9_]+)\s*\(", text)) - {"bl_timer_stats_t"})
 
 
 def test_the_library_exports_every_declared_function():
     lib = hip.lib()
     names = [n for h in HEADERS for n in declared_functions(h)]
-    assert len(names) > 50
+    assert len(names) > 80 and sum(n.startswith("blf_") for n in names) == 34
     missing = [n for n in names if not hasattr(lib, n)]
     assert missing == []
 
@@ -39,6 +40,7 @@ C_LAYOUT = r"""
 #include <stdio.h>
 #include "beatlm_ir.h"
 #include "beatlm_schedule.h"
+#include "beatlm_load.h"
 #define P(T) printf(#T " %zu\n", sizeof(T));
 #define O(T, f) printf(#T "." #f " %zu\n", offsetof(T, f));
 int main(void) {
@@ -49,6 +51,8 @@ int main(void) {
   P(bli_op) P(bli_tensor_desc) P(bli_profile) P(bli_placement) P(bli_kernel_info)
   O(bli_kernel_info, output_start) O(bli_kernel_info, bindings) P(bli_vit_dims) P(bli_block_ids) P(bli_embed_ids)
   P(bls_frame) P(bls_frame_plan) O(bls_frame_plan, runs) O(bls_frame_plan, budget)
+  P(blf_tensor) O(blf_tensor, shape) O(blf_tensor, bytes) P(blf_role) P(blf_spec) O(blf_spec, role)
+  P(blf_dav2_config) O(blf_dav2_config, out_indices) O(blf_dav2_config, factor) O(blf_dav2_config, head_hidden_size)
   return 0;
 }
 """
@@ -68,6 +72,7 @@ def test_the_host_structs_have_the_c_layout(tmp_path):
         "bli_profile": ir.Profile, "bli_placement": ir.Placement, "bli_kernel_info": ir.KernelInfo,
         "bli_vit_dims": ir.VitDims, "bli_block_ids": ir.BlockIds, "bli_embed_ids": ir.EmbedIds,
         "bls_frame": schedule.Frame, "bls_frame_plan": schedule._Plan,
+        "blf_tensor": load._Tensor, "blf_role": load._Role, "blf_spec": load._Spec, "blf_dav2_config": load._Config,
     }
     for name, cls in py.items():
         assert int(got[name]) == C.sizeof(cls), name
