@@ -223,7 +223,8 @@ class Graph:
         self.handle = h
 
     def __del__(self):
-        if getattr(self, "handle", None):
+        # At interpreter exit the module's globals may already be gone.
+        if getattr(self, "handle", None) and callable(_lib):
             _lib().bli_graph_free(self.handle)
             self.handle = None
 

@@ -278,6 +278,55 @@ def vit_block(x, w: dict, t, h, d, mlp, eps, attention_rounded=True):
     return out
 
 
+def depth_decoder(cfg, side, features, w):
+    """The DPT decoder composed from the ops above, as the reference composes
+    it (crates/beatlm-bench/src/reference.rs:194-244 for the residual unit and
+    fusion layer, crates/beatlm/src/model/depth_anything_v2.rs:882-981 for the
+    stages and the head). `cfg` carries the configuration's fields (patch
+    size, hidden size, neck sizes, resamplings, fusion and head widths);
+    `features` the four [grid][grid][hidden] maps; `w` the weights by the
+    checkpoint's names, convolutions HWIO. Returns the [side][side] depth."""
+    grid, F = side // cfg.patch_size, cfg.fusion_hidden_size
+    stages = []
+    for i, feat in enumerate(features):
+        ch = cfg.neck_hidden_sizes[i]
+        pre = f"neck.reassemble_stage.layers.{i}"
+        m = conv1x1(feat, w[pre + ".projection.weight"], w[pre + ".projection.bias"], grid * grid, cfg.hidden_size, ch)
+        kind = cfg.reassemble[i]
+        if kind[0] == "up":
+            f = kind[1]
+            m = conv_transpose(m, w[pre + ".resize.weight"], w[pre + ".resize.bias"], grid, grid, ch, ch, f)
+            hw = (grid * f, grid * f)
+        elif kind[0] == "down":
+            m = conv3x3(m, w[pre + ".resize.weight"], w[pre + ".resize.bias"], grid, grid, ch, ch, kind[1])
+            hw = ((grid - 1) // kind[1] + 1,) * 2
+        else:
+            hw = (grid, grid)
+        stages.append((conv3x3(m, w[f"neck.convs.{i}.weight"], None, hw[0], hw[1], ch, F), hw))
+
+    def unit(x, name, hw):
+        a = conv3x3(relu(x), w[name + ".convolution1.weight"], w[name + ".convolution1.bias"], hw[0], hw[1], F, F)
+        b = conv3x3(relu(a), w[name + ".convolution2.weight"], w[name + ".convolution2.bias"], hw[0], hw[1], F, F)
+        return add(b, x)
+
+    fused, hw_out = None, None
+    for layer, (stage, hw) in enumerate(reversed(stages)):
+        nxt = len(stages) - (layer + 2)
+        out = stages[nxt][1] if nxt >= 0 else (hw[0] * 2, hw[1] * 2)
+        name = f"neck.fusion_stage.layers.{layer}"
+        x = stage if fused is None else add(unit(stage, name + ".residual_layer1", hw), fused)
+        x = unit(x, name + ".residual_layer2", hw)
+        r = resize_bilinear(x, hw[0], hw[1], out[0], out[1], F)
+        fused = conv1x1(r, w[name + ".projection.weight"], w[name + ".projection.bias"], out[0] * out[1], F, F)
+        hw_out = out
+    full = grid * cfg.patch_size
+    first = conv3x3(fused, w["head.conv1.weight"], w["head.conv1.bias"], hw_out[0], hw_out[1], F, F // 2)
+    r = resize_bilinear(first, hw_out[0], hw_out[1], full, full, F // 2)
+    second = relu(conv3x3(r, w["head.conv2.weight"], w["head.conv2.bias"], full, full, F // 2, cfg.head_hidden_size))
+    third = conv1x1(second, w["head.conv3.weight"], w["head.conv3.bias"], full * full, cfg.head_hidden_size, 1)
+    return relu(third)
+
+
 # ---- WGSL-order emulation ----
 
 def wg_gelu_erf(x):

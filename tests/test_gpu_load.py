@@ -71,3 +71,33 @@ def test_a_checkpoint_file_runs_through_the_loader_on_the_gpu(ctx, tmp_path):
     got = ir.run_on_gpu(ctx, g, values)[m.depth]
     bad = oracle.first_mismatch(got, want)
     assert bad is None, f"depth element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
+
+
+@pytest.mark.parametrize("side", [98, 518])
+def test_the_gpu_depth_matches_transformers_on_its_own_state_dict(ctx, side):
+    """transformers' DepthAnythingForDepthEstimation (random parameters, see
+    tests/test_transformers_dav2.py) saved as safetensors, loaded, run on the
+    GPU in f32: the depth within the reference's feature tolerance (max 2e-3,
+    mean 5e-5, load/depth_anything_v2/reference.rs:198-244) scaled by the
+    depth's largest value; at 518 pixels the embedding is used as stored."""
+    torch = pytest.importorskip("torch")
+    pytest.importorskip("transformers")
+    from safetensors.torch import save
+
+    from tests.test_transformers_dav2 import hf_model
+
+    model = hf_model()
+    archive = load.Archive.parse(save({k: v.contiguous() for k, v in model.state_dict().items()}))
+    cfg = ir.DepthConfig.small()
+    g = ir.Graph()
+    m = ir.depth_model(g, cfg, side)
+    values = load.depth_weights(archive, cfg, m, side)
+    image = np.random.default_rng(side).standard_normal((side, side, 3)).astype(np.float32)
+    values[m.encoder.embed.image] = image.ravel()
+    got = ir.run_on_gpu(ctx, g, values)[m.depth]
+    with torch.no_grad():
+        want = model(pixel_values=torch.from_numpy(image).permute(2, 0, 1)[None]).predicted_depth[0].numpy().ravel()
+    scale = float(np.abs(want).max())
+    err = np.abs(got - want)
+    assert scale > 0 and (want > 0).mean() > 0.1
+    assert err.max() <= 2e-3 * scale and err.mean() <= 5e-5 * scale, (err.max(), err.mean(), scale)
