@@ -262,6 +262,33 @@ def layernorm_hbm(ctx, rows: int, width: int, repeats: int = 20) -> dict:
 DEPTH_SIDES_MS = {518: 202.3, 434: 137.8, 350: 85.6, 266: 53.2, 182: 35.0}
 
 
+def depth_decoder_cpu(threads: int) -> dict:
+    """The decoder of Depth Anything V2 Small at 518 pixels composed from the
+    oracle's restatement of the reference's CPU ops (f64 accumulation, OpenMP
+    over output pixels) on the host cores: 1 warm-up, median of 3."""
+    import oracle
+
+    cfg = ir.DepthConfig.small()
+    side, grid = 518, 37
+    g = ir.Graph()
+    for i in range(4):
+        g.tensor(i, ir.INPUT, grid * grid * cfg.hidden_size)
+    _, weights, _ = ir.depth_decoder(g, cfg, side, [0, 1, 2, 3], 10)
+    rng = np.random.default_rng(9)
+    named = {name: (rng.uniform(-0.1, 0.1, n) if name.endswith(".bias") else
+                    rng.uniform(-1, 1, n) / np.sqrt(cfg.fan_in(name))).astype(np.float32) for _, name, n in weights}
+    features = [rng.standard_normal(grid * grid * cfg.hidden_size).astype(np.float32) for _ in range(4)]
+    oracle.depth_decoder(cfg, side, features, named)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        oracle.depth_decoder(cfg, side, features, named)
+        times.append(time.perf_counter() - t0)
+    return {"value": round(statistics.median(times) * 1e3, 1), "unit": "ms/run (decoder)", "cores": threads,
+            "kind": "port", "sample": "the DPT decoder at 518 pixels (37 x 37 features of 4 taps) in the reference's "
+            "CPU ops restated in C (oracle, f64 accumulation), OpenMP; 1 warm-up, median of 3"}
+
+
 def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict:
     """The whole model (12-layer encoder, four tapped feature maps, DPT
     decoder) at each of the reference's five image sides: ms per run over
@@ -315,6 +342,21 @@ def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict
             out["decoder_kernel_ms_at_518"] = round(sum(us[k] for k in dec) / 1e3, 3)
             out["decoder_us_by_kernel_at_518"] = {k: round(v, 1) for k, v in sorted(by_name.items(), key=lambda x: -x[1])}
             out["plan_bytes_at_518"] = prep.plan.total_bytes()
+            # The decoder's dominant kernel family (by main op; the 3 x 3
+            # convolutions): their algorithmic flop over their summed
+            # per-launch time against the matrix cores' peak.
+            fam: dict[int, list[int]] = {}
+            for k in dec:
+                fam.setdefault(prep.program.kernel(k).main, []).append(k)
+            main = max(fam, key=lambda f: sum(us[k] for k in fam[f]))
+            t = sum(us[k] for k in fam[main])
+            flops = sum(kernel_flops(prep.program.kernel(k)) for k in fam[main])
+            peak = PEAK_TFLOPS["f16"] if dtype == hip.F16 else PEAK_TFLOPS["bf16"] / 3.0
+            a = flops / t / 1e6
+            out["decoder_roofline"] = {
+                "kernel": {hip.MAIN_CONV3X3: "conv2d3x3 (all fusions)"}.get(main, str(main)), "launches": len(fam[main]),
+                "bound": "mfma", "achieved": round(a, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
+                "frac": round(a / peak, 4), "us": round(t, 1), "algorithmic_flop": int(flops), "traffic": None}
         del prep
     return out
 
@@ -508,6 +550,9 @@ def main() -> int:
 
     if args.depth_runs > 0:
         result["depth_model"] = depth_model_runs(ctx, args.depth_runs, args.kernel_repeats)
+        if not args.no_cpu_baseline:
+            threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+            result["depth_model"]["cpu_baseline"] = depth_decoder_cpu(threads)
 
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
