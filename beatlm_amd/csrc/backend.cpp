@@ -524,13 +524,21 @@ void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, co
             const uint32_t t = s.bindings[b].tensor;
             if (!is_internal(t)) continue;
             Use &u = use_of(t);
-            bool ok = s.main == BL_MAIN_MATMUL && b == s.reads[0] && t != out_t;
+            // A pipelined GEMM's A, or a 3x3 convolution's image when its
+            // ring kernel takes the fast window gather (channels a whole
+            // k-step, the image under 2^31 elements, 9 cin under 2^16).
+            const bool conv = s.main == BL_MAIN_CONV3X3;
+            bool ok = (s.main == BL_MAIN_MATMUL || conv) && b == s.reads[0] && t != out_t;
             for (uint32_t c = 0; c < last && ok; c++)
                 if (c != b && s.bindings[c].tensor == t) ok = false;  // also an epilogue operand or B
             for (uint32_t si = 0; si < ks->sets && ok; si++) {
                 const Launch &L = ks->kernels[ki].per_set[si];
-                ok = L.family == Family::GEMM && L.math == Math::SPLIT && L.gemm.load == 0 && L.gemm.pipeline &&
-                     L.gemm.k % 32 == 0;
+                const GemmArgs &g = L.gemm;
+                ok = L.family == Family::GEMM && L.math == Math::SPLIT && L.gemm.pipeline &&
+                     (conv ? g.load == 3 && gemm_tile_cols(L.tile) >= 64 && g.p2 % 32 == 0 &&
+                                 (uint64_t)(g.p0 + 1) * (g.p1 + 1) * g.p2 < (1ull << 31) && 9ull * g.p2 < (1u << 16) &&
+                                 !getenv("BL_CONV_NO_SPLIT_INPUT")
+                          : g.load == 0 && g.k % 32 == 0);
             }
             if (ok) u.readers.push_back(ki);
             else u.other = true;
@@ -561,7 +569,9 @@ void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, co
             Kernel &K = ks->kernels[ki];
             K.label += " < split";
             for (Launch &L : K.per_set) {
-                L.gemm.a_planes = (uint64_t)L.gemm.m * L.gemm.k;
+                // The planes split the whole tensor: the image of a convolution.
+                L.gemm.a_planes = L.gemm.load == 3 ? (uint64_t)L.gemm.p0 * L.gemm.p1 * L.gemm.p2 : (uint64_t)L.gemm.m * L.gemm.k;
+                if (L.gemm.load == 3) continue;
                 // Without the split in its k-steps the 32 x 64 tile with 64-wide
                 // steps in a 3-stage ring beats the long-k rule's 64 x 64 tile
                 // with four groups (fc2: 15.7 against 18.8 us).

@@ -164,6 +164,9 @@ def test_a_whole_decoder_matches_the_oracle(ctx, side):
     assert float(np.max(want)) > 0.0  # the final ReLU leaves something to compare
     for parts in (1, 2):
         prep = ir.prepare(ctx, g, ir.FUSION_ON, parts)
+        labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+        # Residual units' second convolutions read their input as bf16 planes.
+        assert any(lab.startswith("conv2d3x3+add") and "< split" in lab for lab in labels), labels
         for tid, v in vals.items():
             prep.write(tid, v)
         prep.run()

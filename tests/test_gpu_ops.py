@@ -242,3 +242,26 @@ def test_the_class_token_position_add_and_token_drop_match_the_oracle(ctx):
     assert len(g.lower()) == 2
     want = oracle.add(oracle.prepend_token(token, patches, TOKENS - 1, WIDTH), positions)[WIDTH:]
     assert_chain_matches(ctx, "class token, position add, token drop", g, {**inputs, "__want__": want})
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(268324, 32, 1, True), (1000, 64, 4, True), (777, 12, 3, False),
+                                        (5, 4, 2, True), (333, 10, 1, True)])
+def test_products_with_few_columns_match_the_oracle(ctx, m, k, n, bias):
+    """At most 4 columns with k a multiple of 4 take the GEMV kernel (the
+    depth head's 1x1 convolution to one channel); k = 10 keeps the tiled
+    GEMM. f32 (1e-4) and f16 (2e-2), whole and in parts, with ReLU after."""
+    a = oracle.uniform(31, m * k, -2.0, 2.0)
+    b = oracle.fan_in_weights(32, k * n, k)
+    vals = {X: a, W: b}
+    if bias:
+        vals[B] = oracle.uniform(33, n, -0.1, 0.1)
+    o = ir.op(ir.OP_MATMUL, [X, W, B if bias else ir.NONE], [m, k, n])
+    g = chain(vals, [o, ir.op(ir.OP_RELU, [H_], [m * n])])
+    labels = ir.prepare(ctx, g).program.names()
+    assert labels == ["matmul+relu"]
+    want = oracle.relu(oracle.matmul(a, b, vals.get(B), m, k, n))
+    for parts in (1, 3):
+        assert_close(ir.run_on_gpu(ctx, g, vals, parts=parts)[Y], want, f"matmul {m}x{k}x{n} parts {parts}")
+    v16 = {t: v.astype(np.float16) for t, v in vals.items()}
+    want16 = oracle.relu(oracle.matmul(*(v16[t].astype(np.float32) if t in v16 else None for t in (X, W, B)), m, k, n))
+    assert max_abs_err(ir.run_on_gpu(ctx, g, v16, dtype=hip.F16)[Y], want16) <= F16_TOL
