@@ -879,10 +879,13 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                             ga.ksplit = (steps + per - 1) / per;
                         }
                     }
-                    if (ga.ksplit > 1) {
-                        partial_bytes = std::max<uint64_t>(partial_bytes, (uint64_t)ga.ksplit * rows * gn * sizeof(float));
-                        split_users.push_back({ki, si});
-                    }
+                }
+                // (Split k for plain products with few tiles measured slower: the
+                // reduce launch and the partial sums cost more than the shorter
+                // k-loops save, 1.00 -> 1.07 ms for the model at 182 pixels.)
+                if (ga.ksplit > 1) {
+                    partial_bytes = std::max<uint64_t>(partial_bytes, (uint64_t)ga.ksplit * rows * gn * sizeof(float));
+                    split_users.push_back({ki, si});
                 }
                 L.gemm = ga;
                 L.tile = chosen;
@@ -1035,7 +1038,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                     Launch &P = ks->kernels[j].per_set[si];
                     if (P.family == Family::FLASH && P.fl.qkv == F.fl.qkv) continue;
                     if (P.family != Family::GEMM || P.gemm.c != F.fl.qkv) break;
-                    if (P.gemm.load != 0 || P.gemm.epi_mode != 0 || P.math != F.math || P.gemm.m != F.fl.tokens ||
+                    if (P.gemm.load != 0 || P.gemm.epi_mode != 0 || P.gemm.ksplit > 1 || P.math != F.math || P.gemm.m != F.fl.tokens ||
                         P.gemm.n != 3 * F.fl.heads * FLASH_HEAD_DIM)
                         ok = false;
                     producers.push_back(j);
