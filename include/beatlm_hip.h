@@ -84,7 +84,8 @@ enum {
     BL_MAIN_PREPEND_TOKEN = 7,    /* dims: rows, channels */
     BL_MAIN_TOKENS_TO_MAP = 8,    /* dims: height, width, channels */
     BL_MAIN_MAP = 9,              /* dims: elements */
-    /* The DPT head's operations (kernel.rs:447-631). */
+    /* The DPT head's operations: MainOp::Conv2d3x3, ConvTranspose2d, ResizeBilinear
+     * (kernel.rs:1412-1417; the ops at kernel.rs:447-631). */
     BL_MAIN_CONV3X3 = 10,         /* dims: height, width, cin, cout, stride, has_bias; NHWC, HWIO weights, padding 1;
                                    * split along output pixels; prologue BL_PRO_RELU allowed */
     BL_MAIN_CONV_TRANSPOSE = 11,  /* dims: height, width, cin, cout, factor, has_bias; kernel = stride = factor;
