@@ -101,3 +101,35 @@ def test_the_gpu_depth_matches_transformers_on_its_own_state_dict(ctx, side):
     err = np.abs(got - want)
     assert scale > 0 and (want > 0).mean() > 0.1
     assert err.max() <= 2e-3 * scale and err.mean() <= 5e-5 * scale, (err.max(), err.mean(), scale)
+
+
+def test_the_f16_model_stays_near_transformers(ctx):
+    """The same comparison with f16 storage (f32 accumulation) at 518 pixels:
+    every weight, the image and every activation rounded to f16 (11-bit
+    significands) through 12 blocks and the decoder. The bound, 1e-2 of the
+    depth's largest value at most and 1e-3 of it on average, is a few times
+    the error measured on this model (max 3.0e-3, mean 1.4e-4 of the scale)."""
+    torch = pytest.importorskip("torch")
+    pytest.importorskip("transformers")
+    from safetensors.torch import save
+
+    from beatlm_amd import hip
+    from tests.test_transformers_dav2 import hf_model
+
+    model = hf_model()
+    archive = load.Archive.parse(save({k: v.contiguous() for k, v in model.state_dict().items()}))
+    cfg = ir.DepthConfig.small()
+    side = 518
+    g = ir.Graph()
+    m = ir.depth_model(g, cfg, side)
+    values = load.depth_weights(archive, cfg, m, side)
+    image = np.random.default_rng(7).standard_normal((side, side, 3)).astype(np.float32)
+    values[m.encoder.embed.image] = image.ravel()
+    got = ir.run_on_gpu(ctx, g, {t: v.astype(np.float16) for t, v in values.items()}, dtype=hip.F16)[m.depth]
+    with torch.no_grad():
+        want = model(pixel_values=torch.from_numpy(image).permute(2, 0, 1)[None]).predicted_depth[0].numpy().ravel()
+    scale = float(np.abs(want).max())
+    err = np.abs(got - want)
+    print(f"f16 depth at 518: max err {err.max() / scale:.2e}, mean {err.mean() / scale:.2e} of scale {scale:.3e}")
+    assert scale > 0 and (want > 0).mean() > 0.1
+    assert err.max() <= 1e-2 * scale and err.mean() <= 1e-3 * scale, (err.max(), err.mean(), scale)
