@@ -289,6 +289,36 @@ def depth_decoder_cpu(threads: int) -> dict:
             "CPU ops restated in C (oracle, f64 accumulation), OpenMP; 1 warm-up, median of 3"}
 
 
+def depth_model_f16_ms(ctx, runs: int, side: int = 518) -> float:
+    """ms per run of the whole model in f16 storage (f32 accumulation) at
+    `side` pixels, random weights of the checkpoint's shapes."""
+    cfg = ir.DepthConfig.small()
+    g = ir.Graph()
+    m = ir.depth_model(g, cfg, side)
+    grid = side // PATCH
+    vals = synthetic_values(dict(CONFIGS["vit-s-518"], grid=grid), m.encoder.embed, m.encoder.blocks, grid * grid + 1,
+                            np.float16, seed=5000 + side)
+    rng = np.random.default_rng(side + 1)
+    vals[m.encoder.final_g] = (1 + 0.1 * rng.normal(0, 1, cfg.hidden_size)).astype(np.float16)
+    vals[m.encoder.final_b] = (0.1 * rng.normal(0, 1, cfg.hidden_size)).astype(np.float16)
+    for tid, name, n in m.decoder_weights:
+        bound = 0.1 if name.endswith(".bias") else 1.0 / np.sqrt(cfg.fan_in(name))
+        vals[tid] = rng.uniform(-bound, bound, n).astype(np.float16)
+    prep = ir.prepare(ctx, g, dtype=hip.F16)
+    for tid, v in vals.items():
+        prep.write(tid, v)
+    prep.run()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(runs):
+        prep.run()
+    ctx.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / runs
+    d = prep.read(m.depth).astype(np.float32)
+    assert np.isfinite(d).all(), "non-finite f16 depth"
+    return round(ms, 3)
+
+
 def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict:
     """The whole model (12-layer encoder, four tapped feature maps, DPT
     decoder) at each of the reference's five image sides: ms per run over
@@ -550,6 +580,7 @@ def main() -> int:
 
     if args.depth_runs > 0:
         result["depth_model"] = depth_model_runs(ctx, args.depth_runs, args.kernel_repeats)
+        result["depth_model"]["f16_ms_per_run_at_518"] = depth_model_f16_ms(ctx, args.depth_runs)
         if not args.no_cpu_baseline:
             threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
             result["depth_model"]["cpu_baseline"] = depth_decoder_cpu(threads)
