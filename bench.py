@@ -289,6 +289,42 @@ def depth_decoder_cpu(threads: int) -> dict:
             "CPU ops restated in C (oracle, f64 accumulation), OpenMP; 1 warm-up, median of 3"}
 
 
+def checkpoint_load() -> dict:
+    """Reading a Depth Anything V2 Small checkpoint (24 785 089 f32
+    parameters, 99 MB, random numbers under the checkpoint's names and
+    shapes, written to a temporary file): ms to read and parse it, to check
+    it against the inventory, and to convert every weight of the 518-pixel
+    model (transposes, Q/K/V side by side, the position embedding through the
+    bicubic resampling)."""
+    import tempfile
+
+    import safetensors.numpy as stn
+
+    from beatlm_amd import load
+
+    cfg = ir.DepthConfig.small()
+    inv = load.inventory(cfg)
+    rng = np.random.default_rng(3)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "dav2-small.safetensors")
+        stn.save_file({sp.name: rng.standard_normal(sp.shape, dtype=np.float32) for sp in inv}, path)
+        size = os.path.getsize(path)
+        t0 = time.perf_counter()
+        archive = load.Archive.open(path)
+        t1 = time.perf_counter()
+        report = inv.check(archive)
+        t2 = time.perf_counter()
+        g = ir.Graph()
+        m = ir.depth_model(g, cfg, 518)
+        weights = load.depth_weights(archive, cfg, m, 518, check=False)
+        t3 = time.perf_counter()
+    assert report.is_exact() and len(weights) > 0
+    return {"file_bytes": size, "parameters": report.file_parameters, "read_and_parse_ms": round((t1 - t0) * 1e3, 1),
+            "check_ms": round((t2 - t1) * 1e3, 2), "convert_ms": round((t3 - t2) * 1e3, 1),
+            "workload": "a DAv2-Small checkpoint file read, checked against the inventory and converted for the "
+                        "518-pixel graph on the host (one thread)"}
+
+
 def depth_model_f16_ms(ctx, runs: int, side: int = 518) -> float:
     """ms per run of the whole model in f16 storage (f32 accumulation) at
     `side` pixels, random weights of the checkpoint's shapes."""
@@ -581,6 +617,7 @@ def main() -> int:
     if args.depth_runs > 0:
         result["depth_model"] = depth_model_runs(ctx, args.depth_runs, args.kernel_repeats)
         result["depth_model"]["f16_ms_per_run_at_518"] = depth_model_f16_ms(ctx, args.depth_runs)
+        result["depth_model"]["checkpoint_load"] = checkpoint_load()
         if not args.no_cpu_baseline:
             threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
             result["depth_model"]["cpu_baseline"] = depth_decoder_cpu(threads)
