@@ -21,8 +21,11 @@ costs call for, deliveries and misses (--frame-loop-frames 0 skips it).
 
 And `depth_model`: the whole Depth Anything V2 Small (the encoder with its four
 tapped feature maps and the DPT decoder) in f32 at the reference's five image
-sides, ms per run beside the reference's published per-run times
-(--depth-runs 0 skips it).
+sides, ms per run beside the reference's published per-run times; at 518
+pixels the encoder's and decoder's kernel times, the decoder's dominant kernel
+family against the matrix cores' peak, its CPU baseline (the oracle), the f16
+model's time, and a full-size checkpoint read, checked and converted on the
+host (--depth-runs 0 skips it).
 """
 
 from __future__ import annotations
