@@ -60,6 +60,19 @@ int hip_fail(bl_ctx *ctx, hipError_t e, const char *what) {
 // plan is valid here unchanged.
 constexpr uint32_t PLACEMENT_ALIGNMENT = 256;
 
+// Whether the process runs under rocprofv3, which sets these for the program
+// it starts. HIP-graph capture and replay is not used there: a host
+// segmentation fault was recorded under rocprofv3 while the depth model's
+// programs were captured, whose cause was not established.
+bool profiler_attached() {
+    static const bool attached = [] {
+        const bool on = getenv("ROCPROF_OUTPUT_PATH") || getenv("ROCPROFILER_LIBRARY_CTOR");
+        if (on) fprintf(stderr, "beatlm: running under rocprofv3: kernel ranges launch one by one, not as HIP graphs\n");
+        return on;
+    }();
+    return attached;
+}
+
 }  // namespace
 
 struct bl_arenas {
@@ -67,9 +80,16 @@ struct bl_arenas {
     char *base = nullptr;
     std::vector<uint64_t> offset, size;
     uint64_t total = 0;
-    // Bumped by every host write: packed copies of weights made before it are stale.
-    uint64_t generation = 1;
+    // Kernels made over these arenas and not yet destroyed. Each holds the
+    // arenas (bl_arenas_destroy frees the memory only after the last of them
+    // is gone, since their launches point into it) and is told of every host
+    // write, so that it remakes the packed copies a write made stale.
+    std::vector<bl_kernels *> users;
+    bool closed = false;
 };
+
+// A host write to bytes [offset, offset + bytes) of an arena.
+static void kernels_written(bl_kernels *k, uint32_t arena, uint64_t offset, uint64_t bytes);
 
 // ---- context ----
 
@@ -224,8 +244,7 @@ extern "C" int bl_arenas_create(bl_ctx *ctx, const uint64_t *sizes, uint32_t n, 
     return BL_OK;
 }
 
-extern "C" void bl_arenas_destroy(bl_arenas *a) {
-    if (!a) return;
+static void arenas_free(bl_arenas *a) {
     if (a->base) {
         hipSetDevice(a->ctx->device);
         hipStreamSynchronize(a->ctx->stream);
@@ -234,6 +253,16 @@ extern "C" void bl_arenas_destroy(bl_arenas *a) {
     bl_ctx *ctx = a->ctx;
     delete a;
     bl_ctx_release(ctx);
+}
+
+extern "C" void bl_arenas_destroy(bl_arenas *a) {
+    if (!a || a->closed) return;
+    a->closed = true;
+    if (a->users.empty()) arenas_free(a);
+}
+
+static void arenas_written(bl_arenas *a, uint32_t arena, uint64_t offset, uint64_t bytes) {
+    for (bl_kernels *k : a->users) kernels_written(k, arena, offset, bytes);
 }
 
 static int check_range(bl_arenas *a, uint32_t arena, uint64_t offset, uint64_t bytes) {
@@ -254,8 +283,15 @@ extern "C" int bl_arenas_write(bl_arenas *a, uint32_t arena, uint64_t offset, co
     hipError_t e = hipMemcpyAsync(a->base + a->offset[arena] + offset, src, bytes, hipMemcpyHostToDevice,
                                   a->ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(a->ctx->stream);
-    a->generation++;
+    arenas_written(a, arena, offset, bytes);
     return e == hipSuccess ? BL_OK : hip_fail(a->ctx, e, "arena write");
+}
+
+extern "C" int bl_arenas_invalidate(bl_arenas *a, uint32_t arena, uint64_t offset, uint64_t bytes) {
+    if (!a) return BL_ERR_INVALID_ARGUMENT;
+    if (int r = check_range(a, arena, offset, bytes)) return r;
+    if (bytes) arenas_written(a, arena, offset, bytes);
+    return BL_OK;
 }
 
 extern "C" int bl_arenas_read(bl_arenas *a, uint32_t arena, uint64_t offset, void *dst, uint64_t bytes) {
@@ -299,6 +335,11 @@ struct Launch {
     Dpt dpt = Dpt::RESIZE;
     DptArgs dp;
     GemvArgs gv;
+    // The output's bytes (what the launch writes, the scratch aside).
+    const char *out_lo = nullptr, *out_hi = nullptr;
+    // A flash kernel whose QKV projections write its K and Vt (fl.prepped):
+    // those projection kernels (one per part).
+    std::vector<uint32_t> kv_producers;
 };
 
 struct Kernel {
@@ -306,9 +347,10 @@ struct Kernel {
     std::vector<Launch> per_set;
 };
 
-// A packed copy of one B operand (a weight matrix), remade when the host has
-// written the arenas since, or before every launch when a kernel of the
-// program writes the bytes it is packed from.
+// A packed copy of one B operand (a weight matrix), remade before the next
+// launch that reads it once the host has written (or invalidated) any of the
+// bytes it is packed from, or before every launch when a kernel of the
+// program writes those bytes.
 struct Pack {
     Math math;
     const void *src;
@@ -316,7 +358,7 @@ struct Pack {
     uint64_t offset, size;
     uint32_t k, n, k_pad, n_pad;
     uint64_t dst_offset;  // into the kernels' pack buffer
-    uint64_t generation = 0;
+    bool stale = true;
     bool dynamic = false;
 };
 
@@ -471,11 +513,24 @@ uint64_t round4(uint64_t bytes) { return (bytes + 3) / 4 * 4; }
 
 }  // namespace
 
+// What the shared attention scratch holds: the K and Vt operands made from
+// the qkv tensor at `qkv` (null: nothing known), written by the projection
+// kernels in `done` (each writes its part's rows) or, when `whole`, by a flash
+// kernel's own prep from all of qkv. Nothing has written qkv's bytes since.
+struct KvState {
+    const void *qkv = nullptr;
+    const char *lo = nullptr, *hi = nullptr;  // qkv's bytes
+    bool whole = false;
+    std::vector<uint32_t> done;
+};
+
 // A range of kernels captured once as a HIP graph and replayed by
-// bl_kernels_encode_range: one submission instead of one per launch.
+// bl_kernels_encode_range: one submission instead of one per launch. `kv`
+// is what the attention scratch holds after a replay.
 struct RangeGraph {
     uint32_t first, count, set;
     hipGraphExec_t exec;
+    KvState kv;
 };
 
 struct bl_kernels {
@@ -487,12 +542,21 @@ struct bl_kernels {
     float *partials = nullptr;  // split-k GEMMs' partial sums, shared as the attention scratch is
     std::vector<Pack> packs;
     void *pack_buffer = nullptr;
+    uint64_t packs_made = 0;
+    KvState kv;
     std::vector<RangeGraph> graphs;
     // Graphs replay fixed launches: not used when a kernel of the program
-    // rewrites a packed weight's source (the pack must rerun in between), or
-    // when BL_NO_GRAPH is set.
+    // rewrites a packed weight's source (the pack must rerun in between),
+    // when BL_NO_GRAPH is set, or under rocprofv3.
     bool graphs_ok = true;
 };
+
+static void kernels_written(bl_kernels *k, uint32_t arena, uint64_t offset, uint64_t bytes) {
+    for (Pack &pk : k->packs)
+        if (pk.arena == arena && offset < pk.offset + pk.size && pk.offset < offset + bytes) pk.stale = true;
+    // The attention scratch is made from qkv: any host write may have changed it.
+    k->kv = KvState{};
+}
 
 namespace {
 
@@ -982,6 +1046,8 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
             }
             }
             if (si == 0) k.label += " @ " + variant;
+            L.out_lo = (const char *)out_ptr;
+            L.out_hi = L.out_lo + s.bindings[s.n_bindings - 1].size;
             k.per_set.push_back(L);
         }
         ks->kernels.push_back(std::move(k));
@@ -1052,12 +1118,15 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                     ga.fl_tpad = F.fl.t_pad;
                 }
                 F.fl.prepped = 1;
+                F.kv_producers.assign(producers.begin(), producers.end());
+                std::sort(F.kv_producers.begin(), F.kv_producers.end());
             }
         }
     }
     if (n_internal && !getenv("BL_NO_SPLIT_ACTIVATIONS")) keep_split_activations(ks, specs, n, internal, n_internal);
-    if (getenv("BL_NO_GRAPH")) ks->graphs_ok = false;
+    if (getenv("BL_NO_GRAPH") || profiler_attached()) ks->graphs_ok = false;
     bl_ctx_retain(ctx);
+    arenas->users.push_back(ks);
     *out = ks;
     return BL_OK;
 }
@@ -1071,9 +1140,15 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
     if (k->partials) hipFree(k->partials);
     if (k->pack_buffer) hipFree(k->pack_buffer);
     bl_ctx *ctx = k->ctx;
+    bl_arenas *a = k->arenas;
+    a->users.erase(std::find(a->users.begin(), a->users.end(), k));
     delete k;
+    // The arenas outlive every kernel pointing into them.
+    if (a->closed && a->users.empty()) arenas_free(a);
     bl_ctx_release(ctx);
 }
+
+extern "C" uint64_t bl_kernels_packs_made(const bl_kernels *k) { return k ? k->packs_made : 0; }
 
 extern "C" uint32_t bl_kernels_len(const bl_kernels *k) { return k ? (uint32_t)k->kernels.size() : 0; }
 extern "C" uint32_t bl_kernels_sets(const bl_kernels *k) { return k ? k->sets : 0; }
@@ -1084,10 +1159,13 @@ extern "C" const char *bl_kernels_label(const bl_kernels *k, uint32_t i) {
 // Packs a GEMM's B when its source may have changed since the last pack.
 static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
     Pack &pk = k->packs[L.pack];
-    if (!pk.dynamic && pk.generation == k->arenas->generation) return hipSuccess;
+    if (!pk.dynamic && !pk.stale) return hipSuccess;
     PackArgs pa{pk.src, (char *)k->pack_buffer + pk.dst_offset, pk.k, pk.n, pk.k_pad, pk.n_pad};
     hipError_t e = launch_pack(pa, pk.math, s);
-    if (e == hipSuccess) pk.generation = k->arenas->generation;
+    if (e == hipSuccess) {
+        pk.stale = false;
+        k->packs_made++;
+    }
     return e;
 }
 
@@ -1108,6 +1186,50 @@ static hipError_t launch(const Launch &L, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
+// Kernel `i`'s launch `L` as the attention scratch's state `kv` requires it,
+// and that state after it. A flash kernel whose K and Vt its projections
+// write (fl.prepped) reads them from the scratch; when the scratch does not
+// hold them (the flash kernel encoded alone, qkv written since by the host
+// or another kernel, or another flash kernel's operands in between) it runs
+// its own prep instead, which makes them from all of qkv.
+static Launch with_kv(const Launch &L, uint32_t i, KvState &kv) {
+    Launch run = L;
+    if (L.family == Family::FLASH && L.fl.prepped) {
+        bool held = kv.qkv == L.fl.qkv && kv.whole;
+        if (kv.qkv == L.fl.qkv && !kv.whole) {
+            held = true;
+            for (uint32_t p : L.kv_producers)
+                if (std::find(kv.done.begin(), kv.done.end(), p) == kv.done.end()) held = false;
+        }
+        if (!held) {
+            run.fl.prepped = 0;
+            kv = KvState{};
+            kv.qkv = L.fl.qkv;
+            kv.lo = (const char *)L.fl.qkv;
+            kv.hi = kv.lo + (uint64_t)3 * L.fl.tokens * L.fl.heads * FLASH_HEAD_DIM * (L.math == Math::F16 ? 2 : 4);
+            kv.whole = true;
+        }
+        return run;
+    }
+    if (L.family == Family::FLASH) {
+        // A flash kernel's own prep overwrites the scratch's operands.
+        if (kv.qkv != L.fl.qkv) kv = KvState{};
+        return run;
+    }
+    if (L.family == Family::GEMM && L.gemm.flash_ops) {
+        if (kv.qkv != L.gemm.c) {
+            kv = KvState{};
+            kv.qkv = L.gemm.c;
+            kv.lo = (const char *)L.gemm.c;
+            kv.hi = kv.lo + (uint64_t)L.gemm.m * L.gemm.n * (L.math == Math::F16 ? 2 : 4);
+        }
+        kv.done.push_back(i);
+        return run;
+    }
+    if (kv.qkv && L.out_lo < kv.hi && kv.lo < L.out_hi) kv = KvState{};
+    return run;
+}
+
 extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, bl_timer *timer, uint32_t tag) {
     if (!k) return BL_ERR_INVALID_ARGUMENT;
     if (kernel >= k->kernels.size()) return fail(k->ctx, BL_ERR_NO_SUCH_KERNEL, "there is no kernel %u", kernel);
@@ -1120,19 +1242,23 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
     }
     const Launch &L = k->kernels[kernel].per_set[set];
     hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
-    if (e == hipSuccess) e = launch(L, s);
+    if (e == hipSuccess) e = launch(with_kv(L, kernel, k->kv), s);
     if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[kernel].label.c_str());
     if (timer && slice >= 0) bl_timer_slice_end(timer, slice, s);
     return BL_OK;
 }
 
 // The range's launches captured on the context's stream, or null when the
-// capture failed (the caller then launches one by one).
-static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set) {
+// capture failed (the caller then launches one by one). The attention
+// scratch is taken to hold nothing when a replay starts, so the graph is
+// right whatever ran before it; `kv` is what it holds after a replay.
+static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, KvState &kv) {
     hipStream_t s = k->ctx->stream;
+    kv = KvState{};
     if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return nullptr;
     hipError_t e = hipSuccess;
-    for (uint32_t i = first; i < first + count && e == hipSuccess; i++) e = launch(k->kernels[i].per_set[set], s);
+    for (uint32_t i = first; i < first + count && e == hipSuccess; i++)
+        e = launch(with_kv(k->kernels[i].per_set[set], i, kv), s);
     hipGraph_t g = nullptr;
     const hipError_t end = hipStreamEndCapture(s, &g);
     hipGraphExec_t exec = nullptr;
@@ -1158,23 +1284,30 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
             hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
             if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
         }
-        hipGraphExec_t exec = nullptr;
+        const RangeGraph *found = nullptr;
         for (const RangeGraph &g : k->graphs)
-            if (g.first == first && g.count == count && g.set == set) exec = g.exec;
-        if (!exec) {
-            exec = capture_range(k, first, count, set);
-            if (exec) k->graphs.push_back({first, count, set, exec});
-            else k->graphs_ok = false;
+            if (g.first == first && g.count == count && g.set == set) found = &g;
+        if (!found) {
+            KvState after;
+            hipGraphExec_t exec = capture_range(k, first, count, set, after);
+            if (exec) {
+                k->graphs.push_back({first, count, set, exec, after});
+                found = &k->graphs.back();
+            } else {
+                k->graphs_ok = false;
+            }
         }
-        if (exec) {
-            hipError_t e = hipGraphLaunch(exec, s);
-            return e == hipSuccess ? BL_OK : hip_fail(k->ctx, e, "graph launch");
+        if (found) {
+            hipError_t e = hipGraphLaunch(found->exec, s);
+            if (e != hipSuccess) return hip_fail(k->ctx, e, "graph launch");
+            k->kv = found->kv;
+            return BL_OK;
         }
     }
     for (uint32_t i = first; i < first + count; i++) {
         const Launch &L = k->kernels[i].per_set[set];
         hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
-        if (e == hipSuccess) e = launch(L, s);
+        if (e == hipSuccess) e = launch(with_kv(L, i, k->kv), s);
         if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
     }
     return BL_OK;
@@ -1189,10 +1322,11 @@ extern "C" int bl_kernels_time(bl_kernels *k, uint32_t kernel, uint32_t set, uin
     hipError_t e = hipEventCreate(&ev[0]);
     if (e == hipSuccess) e = hipEventCreate(&ev[1]);
     const Launch &L = k->kernels[kernel].per_set[set];
-    // The first launch refreshes a packed operand when it must; the timed
-    // ones then run the kernel alone, back to back.
+    // The first launch refreshes a packed operand when it must (and a flash
+    // kernel's scratch operands); the timed ones then run the kernel alone,
+    // back to back, as it runs in its program.
     if (e == hipSuccess && L.pack >= 0) e = refresh_pack(k, L, s);
-    if (e == hipSuccess) e = launch(L, s);
+    if (e == hipSuccess) e = launch(with_kv(L, kernel, k->kv), s);
     if (e == hipSuccess) e = hipEventRecord(ev[0], s);
     for (uint32_t r = 0; r < repeats && e == hipSuccess; r++) e = launch(L, s);
     if (e == hipSuccess) e = hipEventRecord(ev[1], s);

@@ -175,6 +175,7 @@ _SIGNATURES = {
     "bl_arenas_write": (C.c_int, [_VP, C.c_uint32, C.c_uint64, _VP, C.c_uint64]),
     "bl_arenas_read": (C.c_int, [_VP, C.c_uint32, C.c_uint64, _VP, C.c_uint64]),
     "bl_arenas_device_ptr": (C.c_int, [_VP, C.c_uint32, C.c_uint64, C.POINTER(_VP)]),
+    "bl_arenas_invalidate": (C.c_int, [_VP, C.c_uint32, C.c_uint64, C.c_uint64]),
     "bl_kernels_create": (
         C.c_int,
         [_VP, _VP, C.POINTER(Spec), C.c_uint32, C.POINTER(BindingSet), C.c_uint32, C.POINTER(_VP)],
@@ -199,6 +200,7 @@ _SIGNATURES = {
     "bl_timer_invalidate_submitted": (C.c_int, [_VP]),
     "bl_timer_stats": (C.c_int, [_VP, C.POINTER(TimerStats)]),
     "bl_kernels_time": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_float)]),
+    "bl_kernels_packs_made": (C.c_uint64, [_VP]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
 }
 
@@ -295,6 +297,15 @@ class Arenas:
         self.ctx.check(self.ctx._lib.bl_arenas_read(self.handle, arena, offset, out.ctypes.data, out.nbytes))
         return out
 
+    def device_ptr(self, arena: int, offset: int) -> int:
+        p = C.c_void_p()
+        self.ctx.check(self.ctx._lib.bl_arenas_device_ptr(self.handle, arena, offset, C.byref(p)))
+        return int(p.value or 0)
+
+    def invalidate(self, arena: int, offset: int, nbytes: int) -> None:
+        """The host changed these bytes without write() (through device_ptr)."""
+        self.ctx.check(self.ctx._lib.bl_arenas_invalidate(self.handle, arena, offset, nbytes))
+
     def close(self) -> None:
         if self.handle:
             self.ctx._lib.bl_arenas_destroy(self.handle)
@@ -319,8 +330,10 @@ class Kernels:
         internal: list[int] | None = None,
     ):
         """`internal`: tensor ids the host never reads or writes (the program's
-        activations); the backend may keep them in a layout of its own."""
+        activations); the backend may keep them in a layout of its own. The
+        kernels hold `arenas` (the C side frees them after the kernels)."""
         self.ctx = ctx
+        self.arenas = arenas
         arr = (Spec * max(1, len(specs)))(*specs)
         sets = sets or []
         keep = []
@@ -358,6 +371,9 @@ class Kernels:
 
     def encode_all(self, set_index: int = 0) -> None:
         self.ctx.check(self.ctx._lib.bl_kernels_encode_range(self.handle, 0, len(self), set_index))
+
+    def packs_made(self) -> int:
+        return int(self.ctx._lib.bl_kernels_packs_made(self.handle))
 
     def time(self, kernel: int, repeats: int = 20, set_index: int = 0) -> float:
         """Average µs of one launch over `repeats` back-to-back launches."""

@@ -606,9 +606,19 @@ def tensor_desc(tid, dtype, elements, first, last) -> TensorDesc:
 # ---------------------------------------------------------------------------
 
 
+# Job slots (crates/beatlm-host/src/slots.rs:41-151): slot 0 binds the
+# program's own inputs and outputs; every later slot binds stand-ins for them
+# (Program::stand_in), numbered from these bases so they never collide with
+# the program's tensors. Each slot is one binding set of the kernels.
+SLOT_INPUT_BASE = 1 << 16
+SLOT_OUTPUT_BASE = 2 << 16
+MAX_SLOTS = 1 << 16
+
+
 @dataclass
 class Prepared:
-    """A program realised on the device once: plan, arenas, kernels."""
+    """A program realised on the device once: plan, arenas, kernels, and the
+    tensors each job slot reads and writes."""
 
     ctx: hip.Context
     program: Program
@@ -616,23 +626,43 @@ class Prepared:
     arenas: hip.Arenas
     kernels: hip.Kernels
     dtype: int
+    # slot -> {program tensor id: the tensor that slot binds in its place}
+    slot_tensors: list = None
+    elements: dict = None
 
     def np_dtype(self):
         return np.float16 if self.dtype == hip.F16 else np.float32
 
-    def write(self, tid: int, values: np.ndarray) -> None:
+    def slots(self) -> int:
+        return len(self.slot_tensors or [{}])
+
+    def slot_tensor(self, tid: int, slot: int = 0) -> int:
+        """The tensor slot `slot` binds for the program's input or output `tid`."""
+        if not self.slot_tensors:
+            if slot != 0:
+                raise IndexError(f"slot {slot} of a program realised with one slot")
+            return tid
+        return self.slot_tensors[slot].get(tid, tid)
+
+    def write(self, tid: int, values: np.ndarray, slot: int = 0) -> None:
+        tid = self.slot_tensor(tid, slot)
         p = self.plan.placement(tid)
         if p is None:
             raise KeyError(f"tensor {tid} has no placement")
         self.arenas.write(p.arena, p.offset, np.ascontiguousarray(values, dtype=self.np_dtype()))
 
-    def read(self, tid: int) -> np.ndarray:
-        p = self.plan.placement(tid)
-        elements = next(t.elements for t in self.program.tensors() if t.id == tid)
+    def read(self, tid: int, slot: int = 0) -> np.ndarray:
+        elements = self.elements[tid] if self.elements else next(t.elements for t in self.program.tensors() if t.id == tid)
+        p = self.plan.placement(self.slot_tensor(tid, slot))
         return self.arenas.read(p.arena, p.offset, elements, self.np_dtype())
 
     def run(self, set_index: int = 0) -> None:
         self.kernels.encode_all(set_index)
+
+    def close(self) -> None:
+        """Kernels first, then the arenas they point into."""
+        self.kernels.close()
+        self.arenas.close()
 
 
 def prepare(
@@ -642,27 +672,60 @@ def prepare(
     parts: int = 1,
     flash: bool = True,
     dtype: int = hip.F32,
+    slots: int = 1,
 ) -> Prepared:
     """Lower, optionally fuse attention, split every kernel into `parts`, plan
-    against the MI355X profile and build the kernels."""
+    against the MI355X profile (with `slots` job slots) and build the kernels."""
     program = graph.lower(fusion)
     if flash:
         program = program.fuse_attention()
     if parts != 1:
         program = program.split([parts] * len(program))
-    return realise(ctx, program, dtype)
+    return realise(ctx, program, dtype, slots)
 
 
-def realise(ctx: hip.Context, program: Program, dtype: int = hip.F32) -> Prepared:
+def realise(ctx: hip.Context, program: Program, dtype: int = hip.F32, slots: int = 1) -> Prepared:
     """Plan `program` against the MI355X profile in `dtype` storage, allocate
-    its arenas and build its kernels."""
+    its arenas and build its kernels.
+
+    With `slots` > 1, as the reference's Net::new (slots.rs:96-151,
+    :185-240): every input and output of the program gets one stand-in per
+    slot after the first, planned with the program's tensors (live for the
+    whole program, so no slot shares bytes with an activation or another
+    slot), and the kernels get one binding set per slot that rebinds the
+    program's inputs and outputs to that slot's. Activations and weights are
+    shared: jobs of different slots run one after another on the stream."""
+    if not 1 <= slots <= MAX_SLOTS:
+        raise ValueError(f"{slots} slots; a program has between 1 and {MAX_SLOTS}")
     program.set_dtype(dtype)
-    plan = Plan(program.tensors(), profile("mi355x"))
+    tensors = program.tensors()
+    io = [t.id for t in tensors if program.role(t.id) in (INPUT, OUTPUT)]
+    descs = list(tensors)
+    slot_tensors = [{tid: tid for tid in io}]
+    for slot in range(1, slots):
+        mine = {}
+        for i, tid in enumerate(io):
+            base = SLOT_INPUT_BASE if program.role(tid) == INPUT else SLOT_OUTPUT_BASE
+            stand = base + slot * len(io) + i
+            descs.append(program.stand_in(tid, stand))
+            mine[tid] = stand
+        slot_tensors.append(mine)
+    plan = Plan(descs, profile("mi355x"))
     arenas = hip.Arenas(ctx, plan.arenas())
+    sets = None
+    if slots > 1:
+        sets = []
+        for mine in slot_tensors:
+            subs = []
+            for tid, stand in mine.items():
+                p = plan.placement(stand)
+                subs.append(hip.Substitution(tid, stand, p.arena, 0, p.offset, p.size))
+            sets.append(subs)
     # The host never touches activations: the backend may store them its own way.
-    activations = [t.id for t in program.tensors() if program.role(t.id) == ACTIVATION]
-    kernels = hip.Kernels(ctx, arenas, program.specs(plan), internal=activations)
-    return Prepared(ctx, program, plan, arenas, kernels, dtype)
+    activations = [t.id for t in tensors if program.role(t.id) == ACTIVATION]
+    kernels = hip.Kernels(ctx, arenas, program.specs(plan), sets=sets, internal=activations)
+    return Prepared(ctx, program, plan, arenas, kernels, dtype, slot_tensors if slots > 1 else None,
+                    {t.id: t.elements for t in tensors})
 
 
 def run_on_gpu(ctx, graph, values: dict[int, np.ndarray], fusion=FUSION_ON, parts=1, flash=True, dtype=hip.F32):

@@ -235,6 +235,60 @@ def pmc_summary(directory: str) -> str:
     return "\n".join(out) + "\n"
 
 
+def _counter_rows(path: str):
+    """(dispatch key, kernel name, counter, value, start ns, end ns) of a
+    rocprofv3 --pmc run: its run_counter_collection.csv (csv output) or its
+    run_results.db (the default rocpd database)."""
+    import csv
+    import glob
+    import sqlite3
+
+    for f in sorted(glob.glob(os.path.join(path, "**", "run_counter_collection.csv"), recursive=True)):
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                yield ((f, int(r["Dispatch_Id"])), r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"]),
+                       int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+    for f in sorted(glob.glob(os.path.join(path, "**", "*.db"), recursive=True)):
+        db = sqlite3.connect(f)
+        q = "select dispatch_id, kernel_name, counter_name, value, start, end from counters_collection"
+        for d, name, c, v, t0, t1 in db.execute(q):
+            yield (f, d), name, c, float(v), int(t0), int(t1)
+        db.close()
+
+
+def pmc_kernels(directories: list[str]) -> str:
+    """Per-kernel counter summary of rocprofv3 --pmc runs of this bench (one
+    directory per pass): for every kernel (by name and template arguments),
+    its dispatches, mean duration, and each counter's mean per dispatch.
+    MfmaUtil is rocprofv3's derived metric (MFMA busy cycles over GPU-active
+    cycles of all SIMDs, %), MfmaFlops* its MOPS counters x 512, TA_BUSY_avr
+    the texture addressers' busy cycles averaged over the units."""
+    import re
+
+    per: dict[str, dict] = {}
+    for d in directories:
+        for key, name, c, v, t0, t1 in _counter_rows(d):
+            name = re.sub(r"^void ", "", name)
+            name = re.sub(r"bl::\(anonymous namespace\)::", "", name)
+            name = re.sub(r"\(bl::\w+\)$", "", name).replace("(bl::Math)", "M")
+            k = per.setdefault(name, {"ns": {}, "counters": {}})
+            k["ns"][key] = t1 - t0
+            k["counters"].setdefault(c, []).append(v)
+    lines = []
+    for name, k in sorted(per.items(), key=lambda kv: -sum(kv[1]["ns"].values())):
+        ns = list(k["ns"].values())
+        us = sum(ns) / len(ns) / 1e3
+        cs = {c: sum(v) / len(v) for c, v in k["counters"].items()}
+        parts = [f"{name[:72]:72s} dispatches {len(ns):5d}  {us:8.2f} us"]
+        for c in sorted(cs):
+            parts.append(f"{c} {cs[c]:.4g}")
+        flops = cs.get("MfmaFlopsBF16", 0.0) + cs.get("MfmaFlopsF16", 0.0)
+        if flops:
+            parts.append(f"=> matrix cores {flops / us / 1e6:.1f} TFLOP/s ({flops / us / 1e6 / PEAK_TFLOPS['bf16']:.1%} of 2.5 PFLOP/s)")
+        lines.append("  ".join(parts))
+    return "\n".join(lines) + "\n"
+
+
 def layernorm_hbm(ctx, rows: int, width: int, repeats: int = 20) -> dict:
     """One LayerNorm of `rows` x `width` f32 rows, larger than the caches, timed
     alone: algorithmic bytes (read x, write y, read gamma and beta) over the
@@ -251,8 +305,7 @@ def layernorm_hbm(ctx, rows: int, width: int, repeats: int = 20) -> dict:
     prep.write(2, 1 + 0.1 * rng.standard_normal(width, dtype=np.float32))
     prep.write(3, 0.1 * rng.standard_normal(width, dtype=np.float32))
     us = bracketed(ctx, prep, [0], repeats)[0]
-    prep.kernels.close()
-    prep.arenas.close()
+    prep.close()
     nbytes = 4.0 * (2 * rows * width + 2 * width)
     gbs = nbytes / us / 1e3
     return {"rows": rows, "width": width, "dtype": "f32", "algorithmic_bytes_per_launch": int(nbytes),
@@ -354,6 +407,7 @@ def depth_model_f16_ms(ctx, runs: int, side: int = 518) -> float:
     ctx.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / runs
     d = prep.read(m.depth).astype(np.float32)
+    prep.close()
     assert np.isfinite(d).all(), "non-finite f16 depth"
     return round(ms, 3)
 
@@ -426,7 +480,7 @@ def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict
                 "kernel": {hip.MAIN_CONV3X3: "conv2d3x3 (all fusions)"}.get(main, str(main)), "launches": len(fam[main]),
                 "bound": "mfma", "achieved": round(a, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
                 "frac": round(a / peak, 4), "us": round(t, 1), "algorithmic_flop": int(flops), "traffic": None}
-        del prep
+        prep.close()
     return out
 
 
@@ -459,6 +513,101 @@ def cpu_baseline(cfg, tokens, threads):
     return statistics.median(times) * 1e6
 
 
+def oracle_encoder_output(cfg, emb, block_ids, tokens, vals, frames_input=None):
+    """The oracle's encoder (patch embedding, class token and positions, the
+    blocks) over the values the GPU was given, f32 (f16 values widened)."""
+    import oracle
+
+    f = {k: np.asarray(v, np.float32) for k, v in vals.items()}
+    if frames_input is not None:
+        f[emb.image] = np.asarray(frames_input, np.float32)
+    grid, width, heads = cfg["grid"], cfg["width"], cfg["heads"]
+    x = oracle.patch_embed(f[emb.image], f[emb.patch_w], f[emb.patch_b], grid, grid, PATCH, 3, width)
+    x = oracle.add(oracle.prepend_token(f[emb.cls], x, grid * grid, width), f[emb.pos])
+    for ids in block_ids:
+        w = {name: f[getattr(ids, name)] for name in ir.BLOCK_WEIGHTS}
+        x = oracle.vit_block(x, w, tokens, heads, width // heads, 4 * width, EPS, attention_rounded=cfg["dtype"] == "f32")
+    return x
+
+
+def frame_image(cfg, frame: int, np_dtype):
+    """Frame `frame`'s image: U[0,1] normalised, its own seed per frame."""
+    side = cfg["grid"] * PATCH
+    rng = np.random.default_rng(700 + frame)
+    mean = np.array([0.485, 0.456, 0.406], np.float32)
+    std = np.array([0.229, 0.224, 0.225], np.float32)
+    return (((rng.uniform(0, 1, (side, side, 3)).astype(np.float32) - mean) / std).ravel()).astype(np_dtype)
+
+
+def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_math: str, check: bool):
+    """One encoder workload: `frames` frames a step, each through its own job
+    slot (one binding set per frame, as the reference's Net slots), timed over
+    `steps` steps after `warmup`; per-launch kernel times; the attention group
+    against the matrix cores' peak; the output against the oracle."""
+    cfg = CONFIGS[name]
+    dtype = hip.F16 if cfg["dtype"] == "f16" else hip.F32
+    np_dtype = np.float16 if dtype == hip.F16 else np.float32
+    elt = 2 if dtype == hip.F16 else 4
+    frames = cfg["frames"]
+    g, emb, block_ids, tokens = build_encoder(cfg)
+    prep = ir.prepare(ctx, g, dtype=dtype, slots=frames)
+    vals = synthetic_values(cfg, emb, block_ids, tokens, np_dtype)
+    for tid, v in vals.items():
+        prep.write(tid, v)
+    if frames > 1:
+        for f in range(frames):
+            prep.write(emb.image, frame_image(cfg, f, np_dtype), slot=f)
+
+    def step():
+        for f in range(frames):
+            prep.run(f)
+
+    for _ in range(warmup):
+        step()
+    ctx.synchronize()
+    allocs_before = ctx.allocations()
+    packs_before = prep.kernels.packs_made()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    ctx.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert ctx.allocations() == allocs_before, "the frame loop allocated device memory"
+    assert prep.kernels.packs_made() == packs_before, "the frame loop repacked weights"
+    outs = [prep.read(block_ids[-1].output, slot=f).astype(np.float32) for f in range(frames)]
+    assert all(np.isfinite(o).all() for o in outs), "non-finite encoder output"
+
+    ms_per_step = elapsed * 1e3 / steps
+    us_per_block = ms_per_step * 1e3 / (cfg["blocks"] * frames)
+    n_kernels = len(prep.kernels)
+    per_launch = [prep.kernels.time(k, repeats) for k in range(n_kernels)]
+    infos = [prep.program.kernel(k) for k in range(n_kernels)]
+    groups: dict[str, list[int]] = {}
+    for k in range(n_kernels):
+        groups.setdefault(prep.program.name(k), []).append(k)
+    math_name = "f16" if dtype == hip.F16 else ("bf16x3" if f32_math == "split" else "f32")
+    # An f32 product on bf16 matrix cores is three bf16 MFMAs.
+    mfma_peak = PEAK_TFLOPS["f16"] if dtype == hip.F16 else (
+        PEAK_TFLOPS["bf16"] / 3.0 if f32_math == "split" else PEAK_TFLOPS["f32"])
+    out = {
+        "workload": f"{name}: patch embed + {cfg['blocks']} pre-LN ViT blocks, {tokens} tokens, width {cfg['width']}, "
+                    f"{cfg['heads']} heads x 64, MLP {4 * cfg['width']}, {frames} frame(s) per step "
+                    f"(one job slot each), {cfg['dtype']}",
+        "tokens": tokens, "blocks": cfg["blocks"], "frames": frames, "dtype": cfg["dtype"], "matrix_math": math_name,
+        "value": round(us_per_block, 2), "unit": "us/block", "ms_per_step": round(ms_per_step, 4),
+        "kernels_per_frame": n_kernels,
+        "per_kernel_us": {g: round(statistics.mean(per_launch[k] for k in ks), 2) for g, ks in groups.items()},
+        "kernel_sum_us_per_block": round(sum(per_launch) / cfg["blocks"], 2),
+    }
+    if check:
+        want = oracle_encoder_output(cfg, emb, block_ids, tokens, vals)
+        err = float(np.max(np.abs(outs[0].astype(np.float64) - want)))
+        tol = 2e-2 if dtype == hip.F16 else 1e-4
+        out["parity"] = {"max_abs_error": float(f"{err:.3e}"), "tolerance": tol, "within": err <= tol,
+                         "checked": "the timed output (frame 0) against the oracle's encoder over the same values"}
+    return prep, infos, groups, per_launch, mfma_peak, elt, out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -467,8 +616,13 @@ def main() -> int:
     ap.add_argument("--config", default="vit-s-518", choices=sorted(CONFIGS))
     ap.add_argument("--f32-math", default="split", choices=["split", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-check", action="store_true", help="skip comparing the timed output with the oracle")
     ap.add_argument("--kernel-repeats", type=int, default=20)
     ap.add_argument("--pmc-summary", metavar="DIR", help="write the counter summary of a profile directory and exit")
+    ap.add_argument("--pmc-kernels", metavar="DIR", nargs="+",
+                    help="write the per-kernel counter summary of rocprofv3 --pmc runs and exit")
+    ap.add_argument("--other-configs", default="vit-b-518,vit-l-518x4,vit-s-1036",
+                    help="comma-separated configurations also measured into `configs` ('' for none)")
     ap.add_argument("--frame-loop-frames", type=int, default=120)
     ap.add_argument("--depth-runs", type=int, default=20, help="runs of the whole depth model per side (0 skips it)")
     ap.add_argument("--layernorm-rows", type=int, default=262144)
@@ -478,6 +632,9 @@ def main() -> int:
     if args.pmc_summary:
         sys.stdout.write(pmc_summary(args.pmc_summary))
         return 0
+    if args.pmc_kernels:
+        sys.stdout.write(pmc_kernels(args.pmc_kernels))
+        return 0
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
@@ -486,63 +643,19 @@ def main() -> int:
         )
         return 2
 
-    cfg = CONFIGS[args.config]
-    dtype = hip.F16 if cfg["dtype"] == "f16" else hip.F32
-    np_dtype = np.float16 if dtype == hip.F16 else np.float32
-    elt = 2 if dtype == hip.F16 else 4
-
     ctx = hip.Context(0)
     if args.f32_math == "mfma":
         ctx.set_f32_math(hip.F32_MATH_MFMA_F32)
-    g, emb, block_ids, tokens = build_encoder(cfg)
-    prep = ir.prepare(ctx, g, dtype=dtype)
-    vals = synthetic_values(cfg, emb, block_ids, tokens, np_dtype)
-    for tid, v in vals.items():
-        prep.write(tid, v)
-
-    frames = cfg["frames"]
-
-    def step():
-        for _ in range(frames):
-            prep.run()
-
-    for _ in range(args.warmup):
-        step()
-    ctx.synchronize()
-    allocs_before = ctx.allocations()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    ctx.synchronize()
-    elapsed = time.perf_counter() - t0
-    assert ctx.allocations() == allocs_before, "the frame loop allocated device memory"
-    out = prep.read(block_ids[-1].output)
-    assert np.isfinite(out.astype(np.float32)).all(), "non-finite encoder output"
-
-    ms_per_step = elapsed * 1e3 / args.steps
-    blocks_per_step = cfg["blocks"] * frames
-    us_per_block = ms_per_step * 1e3 / blocks_per_step
-
-    # Per-launch durations: each kernel alone, back to back, between a hipEvent
-    # pair on the backend's stream (what a kernel trace reports per dispatch).
-    n_kernels = len(prep.kernels)
-    per_launch = [prep.kernels.time(k, args.kernel_repeats) for k in range(n_kernels)]
-    infos = [prep.program.kernel(k) for k in range(n_kernels)]
-    groups: dict[str, list[int]] = {}
-    for k in range(n_kernels):
-        groups.setdefault(prep.program.name(k), []).append(k)
+    cfg = CONFIGS[args.config]
+    prep, infos, groups, per_launch, mfma_peak, elt, main_line = measure_encoder(
+        ctx, args.config, args.steps, args.warmup, args.kernel_repeats, args.f32_math,
+        check=not args.no_check and args.config != "vit-l-518x4")
     totals = {g: sum(per_launch[k] for k in ks) for g, ks in groups.items()}
     dominant = max(totals, key=totals.get)
-
-    math_name = "f16" if dtype == hip.F16 else ("bf16x3" if args.f32_math == "split" else "f32")
-    # An f32 product on bf16 matrix cores is three bf16 MFMAs.
-    mfma_peak = PEAK_TFLOPS["f16"] if dtype == hip.F16 else (
-        PEAK_TFLOPS["bf16"] / 3.0 if args.f32_math == "split" else PEAK_TFLOPS["f32"]
-    )
-    traffic = read_traffic(args.config, math_name)
+    traffic = read_traffic(args.config, main_line["matrix_math"])
     brackets = []
 
-    def roof(group, tag):
+    def roof(prep, infos, groups, mfma_peak, elt, group, tag, traffic):
         """The group's launches re-timed between two zero-length spin launches,
         which mark the span in a counter profile; achieved = algorithmic work of
         one launch of each kernel over their summed per-launch time."""
@@ -565,39 +678,55 @@ def main() -> int:
         return {"bound": "hbm", "achieved": round(a, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(a / PEAK_HBM_GBS, 4), **common}
 
-    roofline = roof(dominant, "roofline")
-    attn = roof("flash_attention", "attention") if "flash_attention" in groups else None
+    roofline = roof(prep, infos, groups, mfma_peak, elt, dominant, "roofline", traffic)
+    attn = (roof(prep, infos, groups, mfma_peak, elt, "flash_attention", "attention", traffic)
+            if "flash_attention" in groups else None)
+    prep.close()
     result = {
         "metric": METRIC,
-        "value": round(us_per_block, 2),
+        "value": main_line["value"],
         "unit": "us/block",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": main_line["ms_per_step"],
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": cfg["dtype"],
         "data": "synthetic (seeded image U[0,1] normalised, random Xavier weights)",
         "config": {
-            "workload": f"{args.config}: patch embed + {cfg['blocks']} pre-LN ViT blocks, {tokens} tokens, "
-            f"width {cfg['width']}, {cfg['heads']} heads x 64, MLP {4 * cfg['width']}, "
-            f"{frames} frame(s) per step, {cfg['dtype']}",
-            "tokens": tokens,
-            "blocks": cfg["blocks"],
-            "frames": frames,
-            "matrix_math": math_name,
-            "kernels_per_frame": len(prep.kernels),
+            "workload": main_line["workload"],
+            "tokens": main_line["tokens"],
+            "blocks": main_line["blocks"],
+            "frames": main_line["frames"],
+            "matrix_math": main_line["matrix_math"],
+            "kernels_per_frame": main_line["kernels_per_frame"],
         },
         "roofline": roofline,
         "attention": attn,
-        "per_kernel_us": {g: round(statistics.mean(per_launch[k] for k in ks), 2) for g, ks in groups.items()},
-        "kernel_sum_us_per_block": round(sum(per_launch) / cfg["blocks"], 2),
+        "per_kernel_us": main_line["per_kernel_us"],
+        "kernel_sum_us_per_block": main_line["kernel_sum_us_per_block"],
     }
+    if "parity" in main_line:
+        result["parity"] = main_line["parity"]
     if attn:
         result["attention_tflops"] = attn["achieved"]
         result["attention_frac_of_mfma_peak"] = attn["frac"]
+
+    # The other configurations: their own µs/block, and their attention
+    # against the f16 matrix cores' peak (2.5 PFLOP/s dense).
+    others = [c for c in args.other_configs.split(",") if c and c != args.config]
+    if others:
+        result["configs"] = {}
+    for name in others:
+        p2, infos2, groups2, per2, peak2, elt2, line = measure_encoder(
+            ctx, name, max(5, args.steps // 4), max(2, args.warmup // 2), args.kernel_repeats, args.f32_math,
+            check=not args.no_check and name == "vit-b-518")
+        if "flash_attention" in groups2:
+            line["attention"] = roof(p2, infos2, groups2, peak2, elt2, "flash_attention", f"attention_{name}", {})
+        p2.close()
+        result["configs"][name] = line
 
     if args.layernorm_rows > 0:
         ln = layernorm_hbm(ctx, args.layernorm_rows, 384, args.kernel_repeats)
@@ -626,14 +755,14 @@ def main() -> int:
             result["depth_model"]["cpu_baseline"] = depth_decoder_cpu(threads)
 
     if not args.no_cpu_baseline:
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
-        cpu_us = cpu_baseline(cfg, tokens, threads)
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        cpu_us = cpu_baseline(cfg, main_line["tokens"], threads)
         result["cpu_baseline"] = {
             "value": round(cpu_us, 1),
             "unit": "us/block",
             "cores": threads,
             "kind": "port",
-            "sample": f"one f32 block ({tokens} tokens) of the reference's WGSL kernels restated in C "
+            "sample": f"one f32 block ({main_line['tokens']} tokens) of the reference's WGSL kernels restated in C "
             "(oracle, same summation order), OpenMP over rows; 1 warm-up, median of 5",
         }
     result["brackets"] = brackets

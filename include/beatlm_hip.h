@@ -224,14 +224,27 @@ void *bl_ctx_stream(bl_ctx *ctx);
 /* ---- arenas: one hipMalloc for every arena of a plan ---- */
 int bl_arenas_create(bl_ctx *ctx, const uint64_t *arena_sizes, uint32_t n,
                      bl_arenas **out);
+/* Kernels made over the arenas keep them alive (as the reference's Kernels
+ * keep their buffers): destroying the arenas first is allowed, and their
+ * memory is freed when the last of those kernels is destroyed. */
 void bl_arenas_destroy(bl_arenas *arenas);
-/* Ordered on the context's stream; returns when the source may be reused. */
+/* Ordered on the context's stream; returns when the source may be reused.
+ * Packed copies of weights made from the written bytes are remade before the
+ * next launch that reads them; nothing else is repacked. */
 int bl_arenas_write(bl_arenas *arenas, uint32_t arena, uint64_t offset,
                     const void *src, uint64_t bytes);
+/* The host changed bytes [offset, offset + bytes) of an arena without
+ * bl_arenas_write (through bl_arenas_device_ptr): what the kernels derived
+ * from those bytes (packed weights, attention operands) is remade before its
+ * next use, as after bl_arenas_write. No counterpart in the reference, whose
+ * host writes only through queue.write_buffer. */
+int bl_arenas_invalidate(bl_arenas *arenas, uint32_t arena, uint64_t offset,
+                         uint64_t bytes);
 /* Waits for the stream, then copies out. */
 int bl_arenas_read(bl_arenas *arenas, uint32_t arena, uint64_t offset, void *dst,
                    uint64_t bytes);
-/* Device address of a byte of an arena (for hosts that bind their own work). */
+/* Device address of a byte of an arena (for hosts that bind their own work).
+ * A host that writes through it calls bl_arenas_invalidate for those bytes. */
 int bl_arenas_device_ptr(bl_arenas *arenas, uint32_t arena, uint64_t offset,
                          void **out);
 
@@ -251,6 +264,8 @@ int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *sp
                                uint32_t n_specs, const bl_binding_set *sets,
                                uint32_t n_sets, const uint32_t *internal,
                                uint32_t n_internal, bl_kernels **out);
+/* Waits for the context's stream; frees the arenas too when they were
+ * destroyed before and these were their last kernels. */
 void bl_kernels_destroy(bl_kernels *kernels);
 uint32_t bl_kernels_len(const bl_kernels *kernels);
 uint32_t bl_kernels_sets(const bl_kernels *kernels);
@@ -259,14 +274,21 @@ uint32_t bl_kernels_sets(const bl_kernels *kernels);
 const char *bl_kernels_label(const bl_kernels *kernels, uint32_t kernel);
 /* Launches kernel `kernel` with binding set `set` on the context's stream.
  * With a timer, the launch is bracketed by that timer's events for the
- * current frame under `tag`. No allocation, no wait. */
+ * current frame under `tag`. No allocation, no wait.
+ * Each kernel's result depends only on its bindings, whatever was encoded
+ * before it: a flash-attention kernel whose K and V operands its QKV
+ * projection's epilogue wrote into the backend's scratch reads them from
+ * there only when nothing has written qkv since; otherwise (the kernel
+ * encoded alone, a host write, another kernel over those bytes) it makes
+ * them from qkv itself first. */
 int bl_kernels_encode(bl_kernels *kernels, uint32_t kernel, uint32_t set,
                       bl_timer *timer, uint32_t tag);
 /* Launches kernels [first, first + count) in order with binding set `set`.
  * The first call for a (first, count, set) captures the launches as a HIP
  * graph; later calls replay it (weights packs that went stale since are
  * remade first, outside the graph). Programs whose kernels rewrite a packed
- * weight's source, or a process with BL_NO_GRAPH set, launch one by one. */
+ * weight's source, a process with BL_NO_GRAPH set, or one run under
+ * rocprofv3 launch one by one. */
 int bl_kernels_encode_range(bl_kernels *kernels, uint32_t first, uint32_t count,
                             uint32_t set);
 
@@ -276,6 +298,11 @@ int bl_kernels_encode_range(bl_kernels *kernels, uint32_t first, uint32_t count,
  * times kernels only through the slice timer: a measurement aid for per-kernel
  * rooflines, free of the launch gaps a per-slice event pair includes. */
 int bl_kernels_time(bl_kernels *kernels, uint32_t kernel, uint32_t set, uint32_t repeats, float *micros_per_launch);
+/* How many packed weight copies the kernels have made so far (once per
+ * weight at first use, again after the host writes its bytes). No
+ * counterpart in the reference: lets a host check its frame loop repacks
+ * nothing. */
+uint64_t bl_kernels_packs_made(const bl_kernels *kernels);
 
 /* ---- slice timer: hipEvent pairs per slice, a ring of frames ---- */
 #define BL_TIMER_RING_DEPTH 3

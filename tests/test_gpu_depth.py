@@ -1,0 +1,139 @@
+"""The benchmark's encoders at full depth on the GPU against the oracle, at the
+north star's bars: max abs error <= 1e-4 for f32 storage, <= 2e-2 for f16
+storage with f32 accumulation.
+
+- ViT-S/14 at 518 pixels: exactly the benchmark's workload (bench.py's
+  build_encoder and synthetic_values): patch embedding, class token and
+  positions, 12 f32 blocks of 1370 tokens; against the oracle's embeddings
+  followed by 12 chained blocks (crates/beatlm-bench/src/reference.rs:388-425,
+  :520-544; the reference's own encoder test, crates/beatlm-bench/src/vit.rs
+  :240-309, runs one such block).
+- ViT-B/14 at 518 pixels: 12 f16 blocks of 1370 tokens, width 768.
+- ViT-L/14 at 518 pixels, four frames: four job slots of one program, each
+  slot one binding set that rebinds the image and the output
+  (crates/beatlm/src/codegen/kernels.rs:120-170, crates/beatlm-host/src/
+  slots.rs:96-151). Each frame through its slot equals the same frame run
+  alone, bit for bit, and the first two blocks of every frame are checked
+  against the oracle.
+
+Every test prints the maximum absolute error it measured."""
+
+import numpy as np
+import pytest
+
+import bench
+import oracle
+from beatlm_amd import hip, ir
+from tests.blockdata import max_abs_err
+
+pytestmark = pytest.mark.gpu
+
+PATCH = bench.PATCH
+
+
+def oracle_encoder(cfg, emb, block_ids, tokens, vals, blocks=None):
+    """The oracle's embeddings and the first `blocks` blocks, in f32 over the
+    values the GPU was given (f16 values widened exactly)."""
+    f = {k: np.asarray(v, np.float32) for k, v in vals.items()}
+    grid, width, heads = cfg["grid"], cfg["width"], cfg["heads"]
+    x = oracle.patch_embed(f[emb.image], f[emb.patch_w], f[emb.patch_b], grid, grid, PATCH, 3, width)
+    x = oracle.add(oracle.prepend_token(f[emb.cls], x, grid * grid, width), f[emb.pos])
+    for ids in block_ids[: blocks if blocks is not None else len(block_ids)]:
+        w = {name: f[getattr(ids, name)] for name in ir.BLOCK_WEIGHTS}
+        x = oracle.vit_block(x, w, tokens, heads, width // heads, 4 * width, bench.EPS,
+                             attention_rounded=cfg["dtype"] == "f32")
+    return x
+
+
+def run_encoder(ctx, cfg, slots=1, blocks=None, seed=2024):
+    cfg = dict(cfg)
+    if blocks is not None:
+        cfg["blocks"] = blocks
+    g, emb, block_ids, tokens = bench.build_encoder(cfg)
+    dtype = hip.F16 if cfg["dtype"] == "f16" else hip.F32
+    vals = bench.synthetic_values(cfg, emb, block_ids, tokens, np.float16 if dtype == hip.F16 else np.float32, seed)
+    prep = ir.prepare(ctx, g, dtype=dtype, slots=slots)
+    for tid, v in vals.items():
+        prep.write(tid, v)
+    return prep, cfg, emb, block_ids, tokens, vals
+
+
+def test_the_benchmark_workload_vit_s_518_f32_matches_the_oracle_within_1e_4(ctx):
+    prep, cfg, emb, block_ids, tokens, vals = run_encoder(ctx, bench.CONFIGS["vit-s-518"])
+    prep.run()
+    ctx.synchronize()
+    got = prep.read(block_ids[-1].output)
+    want = oracle_encoder(cfg, emb, block_ids, tokens, vals)
+    err = max_abs_err(got, want)
+    print(f"vit-s-518, 12 f32 blocks, 1370 tokens: max abs error {err:.3e} (|want| max {np.abs(want).max():.2f})")
+    bad = oracle.first_mismatch(got, want)
+    assert bad is None, f"element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
+    assert err <= 1e-4, f"max abs error {err:.3e} above 1e-4"
+    prep.close()
+
+
+def test_the_vit_b_518_encoder_in_f16_is_within_2e_2_of_the_oracle(ctx):
+    prep, cfg, emb, block_ids, tokens, vals = run_encoder(ctx, bench.CONFIGS["vit-b-518"])
+    prep.run()
+    ctx.synchronize()
+    got = prep.read(block_ids[-1].output).astype(np.float32)
+    want = oracle_encoder(cfg, emb, block_ids, tokens, vals)
+    err = max_abs_err(got, want)
+    print(f"vit-b-518, 12 f16 blocks, 1370 tokens x 768: max abs error {err:.3e} (|want| max {np.abs(want).max():.2f})")
+    assert err <= 2e-2, f"max abs error {err:.3e} above 2e-2"
+    prep.close()
+
+
+def frame_images(cfg, frames):
+    side = cfg["grid"] * PATCH
+    mean = np.array([0.485, 0.456, 0.406], np.float32)
+    std = np.array([0.229, 0.224, 0.225], np.float32)
+    out = []
+    for f in range(frames):
+        rng = np.random.default_rng(700 + f)
+        out.append((((rng.uniform(0, 1, (side, side, 3)).astype(np.float32) - mean) / std).ravel()).astype(np.float16))
+    return out
+
+
+@pytest.mark.parametrize("blocks", [2, 24])
+def test_four_vit_l_frames_through_four_binding_sets(ctx, blocks):
+    """Config 4's four frames as four job slots. Each slot's output equals the
+    same frame run through a one-slot program, bit for bit, and writing one
+    slot's image leaves the other slots' outputs as they were. At two blocks
+    each frame is also checked against the oracle."""
+    cfg = bench.CONFIGS["vit-l-518x4"]
+    frames = cfg["frames"]
+    prep, cfg2, emb, block_ids, tokens, vals = run_encoder(ctx, cfg, slots=frames, blocks=blocks)
+    assert prep.slots() == frames and prep.kernels.sets() == frames
+    images = frame_images(cfg, frames)
+    for f, im in enumerate(images):
+        prep.write(emb.image, im, slot=f)
+    for f in range(frames):
+        prep.run(f)
+    ctx.synchronize()
+    out = [prep.read(block_ids[-1].output, slot=f) for f in range(frames)]
+    # The frames differ, so their outputs do.
+    assert not np.array_equal(out[0], out[1])
+    # Running slot 2 again after rewriting slot 0's image changes only slot 0's input.
+    prep.write(emb.image, images[3], slot=0)
+    prep.run(2)
+    ctx.synchronize()
+    assert np.array_equal(prep.read(block_ids[-1].output, slot=2), out[2])
+    assert np.array_equal(prep.read(block_ids[-1].output, slot=1), out[1])
+    prep.close()
+
+    single, *_ = run_encoder(ctx, cfg, slots=1, blocks=blocks)
+    for f, im in enumerate(images):
+        single.write(emb.image, im)
+        single.run()
+        ctx.synchronize()
+        alone = single.read(block_ids[-1].output)
+        assert np.array_equal(alone, out[f]), f"frame {f}: its slot's output differs from the frame run alone"
+        if blocks <= 2:
+            v = dict(vals)
+            v[emb.image] = im
+            want = oracle_encoder(cfg2, emb, block_ids, tokens, v)
+            err = max_abs_err(out[f].astype(np.float32), want)
+            print(f"vit-l-518 frame {f}, {blocks} f16 blocks, 1370 tokens x 1024: max abs error {err:.3e}")
+            assert err <= 2e-2, f"frame {f}: max abs error {err:.3e} above 2e-2"
+    single.close()
