@@ -910,13 +910,35 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                     ga.kgroups = 4;
                     ga.stages = 2;
                 }
+                // Products of plain rows in f16 or bf16x3 otherwise take 64-wide
+                // k-steps, so that every staged row is whole 128-byte lines: a
+                // wave's load touching 16 half lines reads a third as fast as
+                // one touching 8 whole lines (15 against 48 bytes per clock per
+                // CU from L2, measured). Two-stage rings, so that 2 to 3
+                // workgroups fit a CU (three for the longest k in f16). The
+                // tiles follow the rounds of workgroups the chip runs: bf16x3
+                // takes 64 x 64 for wide outputs whose tiles fit one round at
+                // two per CU (QKV: 11.4 -> 9.1 us), else 32 x 64 (fc1 17.9 ->
+                // 14.5); f16 takes 64 x 64, or 32 x 64 for square projections
+                // of few rows (ViT-L's QKV 38.4 -> 24.1 us, fc1 54.4 -> 33.0).
+                // With fewer 32 x 64 tiles than CUs (small images) the deeper
+                // rings of 32-wide steps hide more latency and stay.
+                uint32_t kslices = 1;
+                if ((fmath == Math::F16 || fmath == Math::SPLIT) && !patch && !conv && gk % 64 == 0 &&
+                    wgs_of(TILE_32x64) >= ctx->compute_units) {
+                    kslices = 2;
+                    ga.kgroups = 1;
+                    ga.stages = fmath == Math::F16 && gk >= 2048 ? 3 : 2;
+                    if (fmath == Math::F16) chosen = (gn <= 1024 && gk <= 1024 && rows <= 2048) ? TILE_32x64 : TILE_64x64;
+                    else chosen = (gn >= 1024 && w64 <= 2ull * ctx->compute_units) ? TILE_64x64 : TILE_32x64;
+                }
                 if (const char *force = getenv("BL_GEMM_TILE")) {
                     int t = atoi(force);
                     if (t >= 0 && t < TILE_COUNT) chosen = t;
                 }
                 if (const char *force = getenv("BL_GEMM_KGROUPS")) ga.kgroups = (uint32_t)atoi(force);
                 if (const char *force = getenv("BL_GEMM_STAGES")) ga.stages = (uint32_t)atoi(force);
-                ga.kslices = 1;
+                ga.kslices = kslices;
                 if (const char *force = getenv("BL_GEMM_KSLICES")) ga.kslices = (uint32_t)atoi(force);
                 // A 3x3 convolution with fewer tiles than CUs (the decoder's deep,
                 // narrow stages: 6 tiles and 108 k-steps at 19 x 19 x 384 -> 64)
@@ -955,7 +977,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
                           " " + std::to_string(gemm_tile_rows(chosen)) + "x" +
-                          std::to_string(gemm_tile_cols(chosen)) +
+                          std::to_string(gemm_tile_cols(chosen)) + (ga.kslices == 2 ? " bk64" : "") +
                           (ga.kgroups > 1 && !conv ? " k" + std::to_string(ga.kgroups) : std::string()) +
                           (ga.ksplit > 1 ? " splitk" + std::to_string(ga.ksplit) : std::string());
                 break;

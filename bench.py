@@ -235,6 +235,44 @@ def pmc_summary(directory: str) -> str:
     return "\n".join(out) + "\n"
 
 
+def copy_calibration(copies: int = 4, nbytes: int = 256 << 20) -> None:
+    """Device-to-device copies of `nbytes` (the runtime's copy kernel), the
+    known traffic the HBM counters of a profile are scaled by."""
+    import ctypes as C
+
+    rt = C.CDLL("libamdhip64.so")
+    rt.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    rt.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+    rt.hipFree.argtypes = [C.c_void_p]
+    src, dst = C.c_void_p(), C.c_void_p()
+    assert rt.hipMalloc(C.byref(src), nbytes) == 0 and rt.hipMalloc(C.byref(dst), nbytes) == 0
+    assert rt.hipMemset(src, 1, nbytes) == 0
+    for _ in range(copies):
+        assert rt.hipMemcpy(dst, src, nbytes, 3) == 0  # hipMemcpyDeviceToDevice
+    assert rt.hipDeviceSynchronize() == 0
+    rt.hipFree(src)
+    rt.hipFree(dst)
+
+
+def trace_summary(directory: str) -> str:
+    """The per-kernel statistics of a rocprofv3 --kernel-trace --stats run
+    (its run_kernel_stats.csv): calls, mean, min and max duration per
+    dispatch and share of the total, longest first."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(directory, "**", "*kernel_stats.csv"), recursive=True)
+    out = [f"{'kernel':100s} {'calls':>6s} {'avg_us':>8s} {'min_us':>8s} {'max_us':>8s} {'pct':>6s}"]
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                name = r["Name"].replace("void bl::(anonymous namespace)::", "")
+                out.append(f"{name[:100]:100s} {r['Calls']:>6s} {float(r['AverageNs']) / 1e3:8.2f} "
+                           f"{float(r['MinNs']) / 1e3:8.2f} {float(r['MaxNs']) / 1e3:8.2f} {float(r['Percentage']):6.2f}")
+    return "\n".join(out) + "\n"
+
+
 def _counter_rows(path: str):
     """(dispatch key, kernel name, counter, value, start ns, end ns) of a
     rocprofv3 --pmc run: its run_counter_collection.csv (csv output) or its
@@ -261,8 +299,9 @@ def pmc_kernels(directories: list[str]) -> str:
     directory per pass): for every kernel (by name and template arguments),
     its dispatches, mean duration, and each counter's mean per dispatch.
     MfmaUtil is rocprofv3's derived metric (MFMA busy cycles over GPU-active
-    cycles of all SIMDs, %), MfmaFlops* its MOPS counters x 512, TA_BUSY_avr
-    the texture addressers' busy cycles averaged over the units."""
+    cycles of all SIMDs, %); MfmaFlops* its MOPS counters x 512, from which
+    the matrix cores' rate follows; TA busy is TA_BUSY_avr over the GPU-active
+    cycles of one XCD (GRBM_GUI_ACTIVE sums the 8)."""
     import re
 
     per: dict[str, dict] = {}
@@ -274,18 +313,18 @@ def pmc_kernels(directories: list[str]) -> str:
             k = per.setdefault(name, {"ns": {}, "counters": {}})
             k["ns"][key] = t1 - t0
             k["counters"].setdefault(c, []).append(v)
-    lines = []
+    lines = [f"{'kernel':64s} {'disp':>5s} {'us':>8s} {'MfmaUtil%':>9s} {'MFMA TFLOP/s':>12s} {'of 2.5P':>7s} {'TA busy':>7s}"]
     for name, k in sorted(per.items(), key=lambda kv: -sum(kv[1]["ns"].values())):
         ns = list(k["ns"].values())
         us = sum(ns) / len(ns) / 1e3
         cs = {c: sum(v) / len(v) for c, v in k["counters"].items()}
-        parts = [f"{name[:72]:72s} dispatches {len(ns):5d}  {us:8.2f} us"]
-        for c in sorted(cs):
-            parts.append(f"{c} {cs[c]:.4g}")
         flops = cs.get("MfmaFlopsBF16", 0.0) + cs.get("MfmaFlopsF16", 0.0)
-        if flops:
-            parts.append(f"=> matrix cores {flops / us / 1e6:.1f} TFLOP/s ({flops / us / 1e6 / PEAK_TFLOPS['bf16']:.1%} of 2.5 PFLOP/s)")
-        lines.append("  ".join(parts))
+        tf = flops / us / 1e6
+        ta = cs["TA_BUSY_avr"] / (cs["GRBM_GUI_ACTIVE"] / 8) if "TA_BUSY_avr" in cs and cs.get("GRBM_GUI_ACTIVE") else None
+        util = cs.get("MfmaUtil")
+        lines.append(f"{name[:64]:64s} {len(ns):5d} {us:8.2f} " + (f"{util:9.2f} " if util is not None else f"{'':9s} ") +
+                     (f"{tf:12.1f} {tf / PEAK_TFLOPS['bf16']:7.1%} " if flops else f"{'':12s} {'':7s} ") +
+                     (f"{ta:7.1%}" if ta is not None else ""))
     return "\n".join(lines) + "\n"
 
 
@@ -621,6 +660,9 @@ def main() -> int:
     ap.add_argument("--pmc-summary", metavar="DIR", help="write the counter summary of a profile directory and exit")
     ap.add_argument("--pmc-kernels", metavar="DIR", nargs="+",
                     help="write the per-kernel counter summary of rocprofv3 --pmc runs and exit")
+    ap.add_argument("--trace-summary", metavar="DIR", help="write the kernel statistics of a kernel trace and exit")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run 256 MiB device copies (the traffic counters' calibration) and exit")
     ap.add_argument("--other-configs", default="vit-b-518,vit-l-518x4,vit-s-1036",
                     help="comma-separated configurations also measured into `configs` ('' for none)")
     ap.add_argument("--frame-loop-frames", type=int, default=120)
@@ -634,6 +676,12 @@ def main() -> int:
         return 0
     if args.pmc_kernels:
         sys.stdout.write(pmc_kernels(args.pmc_kernels))
+        return 0
+    if args.trace_summary:
+        sys.stdout.write(trace_summary(args.trace_summary))
+        return 0
+    if args.copy_calibration:
+        copy_calibration()
         return 0
     if args.gpus != 1:
         print(
