@@ -40,6 +40,7 @@ SOURCES = [
     "k_gemm_f16.hip",
     "k_flash.hip",
     "k_misc.hip",
+    "static_attention.hip",
     "backend.cpp",
     "timer.cpp",
     "ir.cpp",

@@ -104,6 +104,9 @@ extern "C" int bl_ctx_create(int device_ordinal, bl_ctx **out) {
     if (device_ordinal < 0 || device_ordinal >= count) return BL_ERR_INVALID_ARGUMENT;
     bl_ctx *ctx = new bl_ctx();
     ctx->device = device_ordinal;
+    // Messages are formatted into 512 bytes: with this capacity, setting one
+    // allocates nothing (the allocation-free entry point reports through it).
+    ctx->error.reserve(512);
     if ((e = hipSetDevice(device_ordinal)) != hipSuccess) { delete ctx; return BL_ERR_HIP; }
     hipDeviceProp_t prop;
     if ((e = hipGetDeviceProperties(&prop, device_ordinal)) != hipSuccess) { delete ctx; return BL_ERR_HIP; }
@@ -204,6 +207,9 @@ bool bl_events_counted(bl_ctx *ctx, uint64_t n) {
 }
 
 hipStream_t bl_stream_of(bl_ctx *ctx) { return ctx->stream; }
+int bl_device_of(const bl_ctx *ctx) { return ctx->device; }
+uint32_t bl_compute_units_of(const bl_ctx *ctx) { return ctx->compute_units; }
+uint32_t bl_f32_math_of(const bl_ctx *ctx) { return ctx->f32_math; }
 int bl_fail(bl_ctx *ctx, int code, const char *msg) { return fail(ctx, code, "%s", msg); }
 
 // ---- arenas ----

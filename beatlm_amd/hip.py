@@ -31,6 +31,7 @@ ERR_MISSING_PLACEMENT = -21
 ERR_STAND_IN_SIZE = -22
 ERR_NO_SUCH_KERNEL = -23
 ERR_NO_SUCH_SET = -24
+ERR_TOO_LARGE = -25
 ERR_TIMER_TOO_MANY_SLICES = -30
 ERR_TIMER_NO_FRAME = -31
 ERR_TIMER_CAPACITY = -32
@@ -202,6 +203,7 @@ _SIGNATURES = {
     "bl_kernels_time": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_float)]),
     "bl_kernels_packs_made": (C.c_uint64, [_VP]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
+    "bl_flash_attention_static": (C.c_int, [_VP, _VP, _VP, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]),
 }
 
 _lib = None

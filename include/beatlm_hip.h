@@ -67,6 +67,7 @@ enum {
     BL_ERR_STAND_IN_SIZE = -22,
     BL_ERR_NO_SUCH_KERNEL = -23,
     BL_ERR_NO_SUCH_SET = -24,
+    BL_ERR_TOO_LARGE = -25,            /* the shape needs more than a fixed-size buffer holds */
     /* TimerError (gpu/timer.rs:61-89) */
     BL_ERR_TIMER_TOO_MANY_SLICES = -30,
     BL_ERR_TIMER_NO_FRAME = -31,
@@ -303,6 +304,25 @@ int bl_kernels_time(bl_kernels *kernels, uint32_t kernel, uint32_t set, uint32_t
  * counterpart in the reference: lets a host check its frame loop repacks
  * nothing. */
 uint64_t bl_kernels_packs_made(const bl_kernels *kernels);
+
+/* ---- flash attention that allocates nothing ----
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, hosts that
+ * forbid hipMalloc): the computation of a BL_MAIN_FLASH_ATTENTION kernel,
+ * whole, as bl_kernels_encode runs it when no projection wrote its operands:
+ * qkv [tokens][3][heads][64] (dtype BL_F32, with the context's f32 math, or
+ * BL_F16) into out [tokens][heads * 64], scale as the Scale epilogue's, on
+ * the context's stream. The caller passes device pointers to both. Its
+ * scratch (the K and Vt operands, partial results of split key ranges) is a
+ * static device array of BL_STATIC_SCRATCH_BYTES that the library holds on
+ * each GPU it has run this on until the process ends; a shape needing more
+ * is refused with BL_ERR_TOO_LARGE and a message. Nothing is allocated, the
+ * first call on a device aside, which looks the array's address up (and so
+ * loads the code object holding it). Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU race. */
+#define BL_STATIC_SCRATCH_BYTES (64ull << 20)
+int bl_flash_attention_static(bl_ctx *ctx, const void *qkv, void *out, uint32_t tokens,
+                              uint32_t heads, float scale, uint32_t dtype);
 
 /* ---- slice timer: hipEvent pairs per slice, a ring of frames ---- */
 #define BL_TIMER_RING_DEPTH 3
