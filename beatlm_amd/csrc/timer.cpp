@@ -31,6 +31,8 @@ struct Slot {
     uint64_t frame = 0;
     uint32_t used = 0;
     std::vector<hipEvent_t> events;  // 2 per slice
+    hipEvent_t render[2] = {nullptr, nullptr};
+    int render_state = 0;            // 0 not timed, 1 begun, 2 ended
     hipEvent_t done = nullptr;       // recorded at resolve
     std::vector<uint32_t> tags;
 };
@@ -44,6 +46,7 @@ struct bl_timer {
     std::vector<Slot> slots;
     int open = -1;                 // slot of the frame being recorded, -1 when untimed
     bool frame_open = false;
+    bool render_begun = false;     // the open frame's render pass was requested
     std::deque<int> submitted;     // submission order
     bl_timer_stats_t stats{};
     // What the last collect returned; valid until the next collect.
@@ -74,11 +77,13 @@ extern "C" int bl_timer_create(bl_ctx *ctx, uint32_t max_slices, bl_timer **out)
             }
             created++;
         }
-        if (hipEventCreate(&s.done) != hipSuccess) {
-            bl_timer_destroy(t);
-            return bl_fail(ctx, BL_ERR_HIP, "hipEventCreate");
+        for (hipEvent_t *e : {&s.done, &s.render[0], &s.render[1]}) {
+            if (hipEventCreate(e) != hipSuccess) {
+                bl_timer_destroy(t);
+                return bl_fail(ctx, BL_ERR_HIP, "hipEventCreate");
+            }
+            created++;
         }
-        created++;
     }
     bl_events_counted(ctx, created);
     bl_ctx_retain(ctx);
@@ -93,7 +98,8 @@ extern "C" void bl_timer_destroy(bl_timer *t) {
     for (Slot &s : t->slots) {
         for (hipEvent_t e : s.events)
             if (e) hipEventDestroy(e);
-        if (s.done) hipEventDestroy(s.done);
+        for (hipEvent_t e : {s.done, s.render[0], s.render[1]})
+            if (e) hipEventDestroy(e);
     }
     bl_ctx *ctx = t->retained ? t->ctx : nullptr;
     delete t;
@@ -111,6 +117,7 @@ extern "C" int bl_timer_begin_frame(bl_timer *t, uint64_t frame, uint32_t *timed
     }
     t->stats.frames_begun++;
     t->frame_open = true;
+    t->render_begun = false;
     t->open = -1;
     for (size_t i = 0; i < t->slots.size(); i++) {
         if (t->slots[i].state == State::FREE) {
@@ -126,6 +133,7 @@ extern "C" int bl_timer_begin_frame(bl_timer *t, uint64_t frame, uint32_t *timed
         s.invalid = false;
         s.frame = frame;
         s.used = 0;
+        s.render_state = 0;
     }
     if (timed) *timed = t->open >= 0 ? 1u : 0u;
     return BL_OK;
@@ -151,6 +159,31 @@ int bl_timer_slice_begin(bl_timer *t, uint32_t tag, hipStream_t stream, int *sli
 void bl_timer_slice_end(bl_timer *t, int slice, hipStream_t stream) {
     Slot &s = t->slots[t->open];
     hipEventRecord(s.events[2 * slice + 1], stream);
+}
+
+extern "C" int bl_timer_render_begin(bl_timer *t) {
+    if (!t) return BL_ERR_INVALID_ARGUMENT;
+    if (!t->frame_open) return bl_fail(t->ctx, BL_ERR_TIMER_NO_FRAME, "no frame is open on the timer");
+    if (t->render_begun) return bl_fail(t->ctx, BL_ERR_TIMER_RENDER_TWICE, "the frame's render pass is already timed");
+    t->render_begun = true;
+    if (t->open < 0) return BL_OK;  // untimed frame
+    Slot &s = t->slots[t->open];
+    if (hipEventRecord(s.render[0], bl_stream_of(t->ctx)) != hipSuccess)
+        return bl_fail(t->ctx, BL_ERR_HIP, "hipEventRecord");
+    s.render_state = 1;
+    return BL_OK;
+}
+
+extern "C" int bl_timer_render_end(bl_timer *t) {
+    if (!t) return BL_ERR_INVALID_ARGUMENT;
+    if (!t->frame_open) return bl_fail(t->ctx, BL_ERR_TIMER_NO_FRAME, "no frame is open on the timer");
+    if (t->open < 0) return BL_OK;
+    Slot &s = t->slots[t->open];
+    if (s.render_state != 1) return bl_fail(t->ctx, BL_ERR_INVALID_ARGUMENT, "the render pass was not begun");
+    if (hipEventRecord(s.render[1], bl_stream_of(t->ctx)) != hipSuccess)
+        return bl_fail(t->ctx, BL_ERR_HIP, "hipEventRecord");
+    s.render_state = 2;
+    return BL_OK;
 }
 
 extern "C" int bl_timer_resolve(bl_timer *t, uint32_t *resolved) {
@@ -210,6 +243,13 @@ extern "C" int bl_timer_collect(bl_timer *t, bl_frame_timing *out, uint32_t cap,
                 f.failed = 0;
                 f.tags = t->out_tags.back().data();
                 f.micros = t->out_micros.back().data();
+                f.has_render = 0;
+                f.render_micros = 0.0f;
+                float ms = 0.0f;
+                if (s.render_state == 2 && hipEventElapsedTime(&ms, s.render[0], s.render[1]) == hipSuccess) {
+                    f.has_render = 1;
+                    f.render_micros = ms * 1000.0f;
+                }
                 (*n_out)++;
                 t->stats.frames_timed++;
             }

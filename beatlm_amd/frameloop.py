@@ -164,6 +164,21 @@ def calibrate(ctx, graph, values, output_tid, dtype, period_us, render_us, bound
     return Calibration(durations, parts, program, cost, reference_output)
 
 
+def reference_outputs(ctx, graph, values, output_tid, dtype, input_tid, inputs) -> list:
+    """The unsplit program's output for each of `inputs` (one job slot each)."""
+    whole = ir.prepare(ctx, graph, dtype=dtype, slots=len(inputs))
+    try:
+        for tid, v in values.items():
+            whole.write(tid, v)
+        for j, x in enumerate(inputs):
+            whole.write(input_tid, x, slot=j)
+            whole.run(j)
+        ctx.synchronize()
+        return [whole.read(output_tid, slot=j).astype(np.float32) for j in range(len(inputs))]
+    finally:
+        _release(whole)
+
+
 def latency_for(estimates, budget_us: int, expected_us: int) -> int:
     """The smallest FixedLatency that keeps a lone job of slices priced at
     `estimates`: the last frame the scheduler's projection (schedule.rs:381-406)
@@ -182,64 +197,121 @@ def latency_for(estimates, budget_us: int, expected_us: int) -> int:
 
 
 def run(ctx, graph, values, output_tid, dtype, frames=120, period_us=FRAME_PERIOD_US, render_us=8_000,
-        margin_us=0, bound_us=DEFAULT_MAX_DISPATCH_US, tolerance=2e-2) -> dict:
-    """Calibrates, then runs `frames` paced frames; returns the report."""
+        margin_us=0, bound_us=DEFAULT_MAX_DISPATCH_US, tolerance=2e-2, policy: S.Policy | None = None,
+        owed_every: int = 1, slots: int | None = None, input_tid: int | None = None, slot_inputs=None) -> dict:
+    """Calibrates, then runs `frames` paced frames through the host's frame
+    step (S.FrameStep, beatlm-host/src/step.rs:347-467), as the reference
+    bench's engine ticks (crates/beatlm-bench/src/engine.rs:351-470):
+
+      plan(frame, owed) -> encode each run into its job's slot, every compute
+      pass and the render pass timed -> resolve, submit -> after_submit ->
+      collect the frames whose timings have come back (never waiting) ->
+      absorb each -> complete(frame).
+
+    `policy` is FixedLatency{k} by default, with k the smallest that keeps a
+    lone job of the calibrated costs (the latency the bench reports); an
+    OnBeat policy delivers each job on the beat after its submission. A frame
+    owes an input when its index is a multiple of `owed_every`. Jobs run in
+    `slots` job slots (binding sets of the program's input and output, job j
+    in slot j mod slots), by default as many as jobs can be in flight;
+    `slot_inputs` gives each slot's input tensor `input_tid` its own values.
+    Returns the report, with every slot's output against the unsplit
+    program's for the same input."""
     budget = S.budget_for_frame(period_us, render_us, margin_us)
     cal = calibrate(ctx, graph, values, output_tid, dtype, period_us, render_us, bound_us)
     n = len(cal.program)
     estimates = [cal.cost.planning_estimate(i) for i in range(n)]
     k = latency_for(estimates, budget, budget)
+    if policy is None:
+        policy = S.Policy.fixed_latency(k)
+    if slots is None:
+        in_flight = policy.max_in_flight()
+        slots = (S.jobs_with_slices(S.SUBMIT_EVERY, S.IN_FLIGHT_LATENCY, in_flight) if in_flight is not None else None) or 2
+    slots = max(1, min(slots, 64))
+    capacity = S.timer_capacity(n, slots)
+    if capacity is None:
+        raise ValueError(f"{n} slices of {slots} jobs exceed the slice timer")
 
-    prep = ir.realise(ctx, cal.program, dtype)
+    prep = ir.realise(ctx, cal.program, dtype, slots=slots)
     for tid, v in values.items():
         prep.write(tid, v)
-    timer = hip.Timer(ctx, min(4096, n * (k + 1)))
-    sched = S.Scheduler(k, S.MISS_HOLD_PREVIOUS, budget)
+    # Every slot's inputs (the program's INPUT tensors), as slot 0's.
+    program_inputs = [t.id for t in cal.program.tensors() if cal.program.role(t.id) == ir.INPUT]
+    for j in range(1, slots):
+        for tid in program_inputs:
+            prep.write(tid, values[tid], slot=j)
+    inputs = [values[input_tid]] * slots if input_tid is not None else None
+    if slot_inputs is not None:
+        inputs = [slot_inputs[j % len(slot_inputs)] for j in range(slots)]
+        for j in range(slots):
+            prep.write(input_tid, inputs[j], slot=j)
+    timer = hip.Timer(ctx, min(4096, capacity + 1))
+    step = S.FrameStep(policy, S.MISS_HOLD_PREVIOUS, n, margin_us, period_us, cal.cost, S.SUBMIT_EVERY)
     pacer = Pacer(period_us)
-    runs_per_frame, spent, gpu_us_per_frame, frame_wall_us = [], [], [], []
-    delivered = missed = 0
-    job_slices: dict[int, int] = {}
-    job_gpu: dict[int, float] = {}
-    job_of_frame: dict[int, list] = {}
+    runs_per_frame, frame_wall_us, deliveries, misses, spent = [], [], [], [], []
+    tags: dict[int, list] = {}
+    # First use (packing the weights) before the loop, as the reference's
+    # engine warms up before its first frame.
+    prep.run(0)
+    ctx.synchronize()
     allocs = ctx.allocations()
+    packs = prep.kernels.packs_made()
+
+    def absorb_ready():
+        for frame, slices, render in timer.collect(render=True):
+            owners = tags.pop(frame, [])
+            compute = []
+            for tag, us in slices:
+                job, slice_id, planned = owners[tag]
+                compute.append(S.TimedSlice(job, slice_id, int(round(us)), planned))
+            step.absorb(frame, compute, None if render is None else int(round(render)))
+
     try:
-        for _ in range(frames):
+        for f in range(frames):
             index, start = pacer.next()
             began = time.perf_counter()
-            info = S.Frame(index, start, period_us)
-            job = sched.submit(info, list(range(n)), cal.cost)
-            plan = sched.plan_frame(info, budget, cal.cost)
+            planned = step.plan(S.Frame(index, index * period_us, period_us), index % owed_every == 0)
+            spent.append(planned.plan.spent_estimate)
             timer.begin_frame(index)
-            job_of_frame[index] = []
-            for r in plan.runs:
-                prep.kernels.encode(r.slice, 0, timer, r.slice)
-                job_of_frame[index].append(r.job)
+            owners = []
+            for r in planned.plan.runs:
+                owners.append((r.job, r.slice, step.tag(r.slice)))
+                prep.kernels.encode(r.slice, r.job % slots, timer, len(owners) - 1)
+            tags[index] = owners
+            # The render pass, timed apart from the compute passes.
+            timer.render_begin()
             ctx.spin(render_us)
+            timer.render_end()
             timer.submitted(timer.resolve())
-            ctx.synchronize()
-            frame_wall_us.append((time.perf_counter() - began) * 1e6)
+            step.after_submit(index)
+            absorb_ready()
+            plan = step.complete(index)
             runs_per_frame.append(len(plan.runs))
-            spent.append(plan.spent_estimate)
-            delivered += len(plan.delivered)
-            missed += len(plan.missed)
-            job_slices[job] = n
-            for frame, slices in timer.collect():
-                owners = job_of_frame.pop(frame, [])
-                gpu_us_per_frame.append(sum(us for _, us in slices))
-                for (tag, us), owner in zip(slices, owners):
-                    cal.cost.record(tag, int(round(us)))
-                    job_gpu[owner] = job_gpu.get(owner, 0.0) + us
+            deliveries += [(d.job, index) for d in plan.delivered]
+            misses += [(m.job, index) for m in plan.missed]
+            frame_wall_us.append((time.perf_counter() - began) * 1e6)
+        ctx.synchronize()
+        absorb_ready()
+        tally = step.finish()
         stats = timer.stats()
         assert ctx.allocations() == allocs, "the frame loop allocated device memory"
-        out = prep.read(output_tid).astype(np.float32)
+        assert prep.kernels.packs_made() == packs, "the frame loop repacked weights"
+        outs = [prep.read(output_tid, slot=j).astype(np.float32) for j in range(slots)]
     finally:
         timer.close()
         _release(prep)
-    err = float(np.max(np.abs(out - cal.reference_output)))
-    job_times = [v for j, v in job_gpu.items() if j < max(job_gpu, default=0)]
+    if inputs is not None and slot_inputs is not None:
+        wants = reference_outputs(ctx, graph, values, output_tid, dtype, input_tid, inputs)
+    else:
+        wants = [cal.reference_output] * slots
+    err = max(float(np.max(np.abs(o - w))) for o, w in zip(outs, wants))
     split_kernels = sum(1 for p in cal.parts if p > 1)
+    kind = {S.POLICY_FIXED_LATENCY: f"FixedLatency {policy.frames}", S.POLICY_SAME_FRAME: "SameFrame",
+            S.POLICY_ON_BEAT: f"OnBeat (beat {policy.grid_beat} us, margin {policy.margin} us)"}[policy.kind]
     return {
-        "workload": "frame-budget slices at a fixed frame period beside a fixed-time render load",
+        "workload": "frame-budget slices at a fixed frame period beside a fixed-time render load, "
+                    "driven by the host's frame step",
+        "policy": kind,
         "frame_period_us": period_us,
         "render_load_us": render_us,
         "margin_us": margin_us,
@@ -251,7 +323,8 @@ def run(ctx, graph, values, output_tid, dtype, frames=120, period_us=FRAME_PERIO
         "calibrated_job_us": sum(cal.durations),
         "planned_job_us": sum(estimates),
         "latency_frames_k": k,
-        "submit": "every frame",
+        "job_slots": slots,
+        "submit": "every frame" if owed_every == 1 else f"every {owed_every} frames",
         "frames": frames,
         "slices_per_frame": {
             "mean": round(statistics.mean(runs_per_frame), 2),
@@ -259,11 +332,19 @@ def run(ctx, graph, values, output_tid, dtype, frames=120, period_us=FRAME_PERIO
             "max": max(runs_per_frame),
         },
         "spent_estimate_us_per_frame_max": max(spent),
-        "measured_slice_us_per_frame_median": round(statistics.median(gpu_us_per_frame), 1) if gpu_us_per_frame else None,
-        "measured_job_us_median": round(statistics.median(job_times), 1) if job_times else None,
         "frame_wall_us_median": round(statistics.median(frame_wall_us), 1),
-        "delivered": delivered,
-        "missed": missed,
+        "submitted": int(tally.submitted),
+        "delivered": int(tally.delivered),
+        "missed": int(tally.missed),
+        "startup_missed": int(tally.startup_missed),
+        "latency_violations": int(tally.violations),
+        "pending_at_end": int(tally.pending_at_end),
+        "latencies_frames": sorted(set(int(x) for x in tally.latencies)),
+        "dispatches_per_job": sorted(set(int(x) for x in tally.dispatches_per_job)),
+        "gpu_frame_us_median": round(statistics.median(tally.gpu_frame_us), 1) if tally.gpu_frame_us else None,
+        "longest_dispatch_us_max": max(tally.longest_dispatch_us) if tally.longest_dispatch_us else None,
+        "deliveries": deliveries,
+        "misses": misses,
         "dropped_periods": pacer.dropped,
         "timer": {"frames_timed": int(stats.frames_timed), "frames_skipped": int(stats.frames_skipped),
                   "frames_failed": int(stats.frames_failed), "frames_dropped": int(stats.frames_dropped)},

@@ -35,6 +35,7 @@ ERR_TOO_LARGE = -25
 ERR_TIMER_TOO_MANY_SLICES = -30
 ERR_TIMER_NO_FRAME = -31
 ERR_TIMER_CAPACITY = -32
+ERR_TIMER_RENDER_TWICE = -33
 
 # main operations
 MAIN_LAYER_NORM = 1
@@ -146,6 +147,8 @@ class FrameTiming(C.Structure):
         ("failed", C.c_uint32),
         ("tags", C.POINTER(C.c_uint32)),
         ("micros", C.POINTER(C.c_float)),
+        ("has_render", C.c_uint32),
+        ("render_micros", C.c_float),
     ]
 
 
@@ -196,6 +199,8 @@ _SIGNATURES = {
     "bl_timer_destroy": (None, [_VP]),
     "bl_timer_begin_frame": (C.c_int, [_VP, C.c_uint64, C.POINTER(C.c_uint32)]),
     "bl_timer_resolve": (C.c_int, [_VP, C.POINTER(C.c_uint32)]),
+    "bl_timer_render_begin": (C.c_int, [_VP]),
+    "bl_timer_render_end": (C.c_int, [_VP]),
     "bl_timer_submitted": (C.c_int, [_VP, C.c_uint32]),
     "bl_timer_collect": (C.c_int, [_VP, C.POINTER(FrameTiming), C.c_uint32, C.POINTER(C.c_uint32)]),
     "bl_timer_invalidate_submitted": (C.c_int, [_VP]),
@@ -417,13 +422,25 @@ class Timer:
     def submitted(self, resolved: int) -> None:
         self.ctx.check(self.ctx._lib.bl_timer_submitted(self.handle, resolved))
 
-    def collect(self, cap: int = 16) -> list[tuple[int, list[tuple[int, float]]]]:
+    def render_begin(self) -> None:
+        self.ctx.check(self.ctx._lib.bl_timer_render_begin(self.handle))
+
+    def render_end(self) -> None:
+        self.ctx.check(self.ctx._lib.bl_timer_render_end(self.handle))
+
+    def collect(self, cap: int = 16, render: bool = False):
+        """The frames whose timings came back: (frame, [(tag, µs)]), or with
+        `render` (frame, [(tag, µs)], render µs or None)."""
         out = (FrameTiming * cap)()
         n = C.c_uint32()
         self.ctx.check(self.ctx._lib.bl_timer_collect(self.handle, out, cap, C.byref(n)))
         frames = []
         for f in out[: n.value]:
-            frames.append((int(f.frame), [(int(f.tags[i]), float(f.micros[i])) for i in range(f.n_slices)]))
+            slices = [(int(f.tags[i]), float(f.micros[i])) for i in range(f.n_slices)]
+            if render:
+                frames.append((int(f.frame), slices, float(f.render_micros) if f.has_render else None))
+            else:
+                frames.append((int(f.frame), slices))
         return frames
 
     def invalidate_submitted(self) -> int:

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define BL_ABI_VERSION 2u
+#define BL_ABI_VERSION 3u
 #define BL_MAX_EPILOGUE 8
 #define BL_MAX_BINDINGS 8
 
@@ -71,7 +71,8 @@ enum {
     /* TimerError (gpu/timer.rs:61-89) */
     BL_ERR_TIMER_TOO_MANY_SLICES = -30,
     BL_ERR_TIMER_NO_FRAME = -31,
-    BL_ERR_TIMER_CAPACITY = -32
+    BL_ERR_TIMER_CAPACITY = -32,
+    BL_ERR_TIMER_RENDER_TWICE = -33    /* TimerError::RenderPassAlreadyTimed */
 };
 
 /* ---- main operations (MainOp, kernel.rs:1393-1445) ---- */
@@ -332,6 +333,8 @@ typedef struct {
     uint32_t failed;      /* 1: the frame was invalidated and carries no times */
     const uint32_t *tags; /* n_slices tags, valid until the next collect */
     const float *micros;  /* n_slices durations in microseconds */
+    uint32_t has_render;  /* 1: the frame timed its render pass (FrameTiming::render) */
+    float render_micros;
 } bl_frame_timing;
 
 typedef struct {
@@ -343,6 +346,12 @@ void bl_timer_destroy(bl_timer *timer);
 /* Opens a frame. `*timed` is 0 when its ring slot is still in flight: the
  * frame then runs untimed and counts as skipped (FrameTimestamps::is_timed). */
 int bl_timer_begin_frame(bl_timer *timer, uint64_t frame, uint32_t *timed);
+/* FrameTimestamps::render_pass (gpu/timer.rs:527-560): the frame's render
+ * pass, the host's own work on the context's stream enqueued between these
+ * two calls, timed apart from the compute passes (at most once a frame;
+ * nothing is recorded when the frame is untimed). */
+int bl_timer_render_begin(bl_timer *timer);
+int bl_timer_render_end(bl_timer *timer);
 /* Closes the open frame; `*resolved` names it for bl_timer_submitted. */
 int bl_timer_resolve(bl_timer *timer, uint32_t *resolved);
 /* The host says the frame's work reached the stream. A resolved frame never

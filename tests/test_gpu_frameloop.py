@@ -5,6 +5,7 @@ slices), on a small block so each test takes seconds."""
 
 import time
 
+import numpy as np
 import pytest
 
 import oracle
@@ -184,3 +185,38 @@ def test_the_frame_loop_delivers_every_frame_within_its_latency(ctx, small, boun
         assert report["kernels_split"] > 0 and report["slices_per_job"] > report["kernels_unsplit"]
     else:
         assert report["slices_per_job"] == report["kernels_unsplit"]
+
+
+def test_on_beat_delivers_every_job_on_its_beat_at_the_high_resolution_shape(ctx):
+    """Config 5's encoder (ViT-S/14 at 1036 pixels: 5477 tokens, 12 f16
+    blocks) driven by the host's frame step with the OnBeat policy at 60
+    frames per second beside an 8 ms render load: an input every 6 frames,
+    beats every 6 frames, each job delivered by the frame that starts on the
+    beat after its submission (beatlm-host/src/step.rs:686-760 scripts the
+    same), none missed; kernels longer than 40 us split into parts, and each
+    of the two job slots' outputs equals the unsplit program's for its input."""
+    import bench
+    from beatlm_amd import schedule as S
+
+    cfg = bench.CONFIGS["vit-s-1036"]
+    g, emb, ids, tokens = bench.build_encoder(cfg)
+    vals = bench.synthetic_values(cfg, emb, ids, tokens, np.float16)
+    period = 16_667
+    beat = 6 * period
+    frames = 42
+    policy = S.Policy.on_beat(0, beat, 1_000)
+    images = [bench.frame_image(cfg, f, np.float16) for f in range(2)]
+    report = frameloop.run(ctx, g, vals, ids[-1].output, hip.F16, frames=frames, period_us=period, render_us=8_000,
+                           bound_us=40, tolerance=2e-2, policy=policy, owed_every=6, slots=2,
+                           input_tid=emb.image, slot_inputs=images)
+    print({k: report[k] for k in ("policy", "kernels_split", "slices_per_job", "delivered", "missed", "submitted",
+                                  "pending_at_end", "latencies_frames", "output_max_abs_vs_unsplit")})
+    assert report["kernels_split"] > 0 and report["slices_per_job"] > report["kernels_unsplit"]
+    assert report["submitted"] == frames // 6
+    assert report["missed"] == 0, report["misses"]
+    # Every job but the last (due after the run) is delivered, on a beat frame,
+    # six frames after its submission.
+    assert report["delivered"] == report["submitted"] - report["pending_at_end"] >= frames // 6 - 1
+    assert all(frame % 6 == 0 for _, frame in report["deliveries"]), report["deliveries"]
+    assert report["latencies_frames"] == [6]
+    assert report["output_within_tolerance"], report["output_max_abs_vs_unsplit"]
