@@ -26,6 +26,7 @@ struct bl_ctx {
     hipStream_t stream = nullptr;
     std::string error;
     uint64_t allocations = 0;
+    uint64_t device_bytes = 0;  // held now by the context's arenas and kernels
     uint32_t f32_math = BL_F32_MATH_SPLIT_BF16;
     uint32_t compute_units = 0;
     uint32_t wall_clock_khz = 0;
@@ -189,6 +190,7 @@ extern "C" int bl_ctx_synchronize(bl_ctx *ctx) {
 }
 
 extern "C" uint64_t bl_ctx_allocations(const bl_ctx *ctx) { return ctx ? ctx->allocations : 0; }
+extern "C" uint64_t bl_ctx_device_bytes(const bl_ctx *ctx) { return ctx ? ctx->device_bytes : 0; }
 
 extern "C" void *bl_ctx_stream(bl_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
@@ -198,7 +200,14 @@ void *bl_device_alloc(bl_ctx *ctx, uint64_t bytes) {
     void *p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
     ctx->allocations++;
+    ctx->device_bytes += bytes;
     return p;
+}
+
+void bl_device_free(bl_ctx *ctx, void *p, uint64_t bytes) {
+    if (!p) return;
+    hipFree(p);
+    ctx->device_bytes -= bytes;
 }
 
 bool bl_events_counted(bl_ctx *ctx, uint64_t n) {
@@ -236,14 +245,11 @@ extern "C" int bl_arenas_create(bl_ctx *ctx, const uint64_t *sizes, uint32_t n, 
     a->total = total;
     if (total) {
         // One allocation for every arena of the plan.
-        void *p = nullptr;
-        hipError_t e = hipMalloc(&p, total);
-        if (e != hipSuccess) {
+        a->base = (char *)bl_device_alloc(ctx, total);
+        if (!a->base) {
             delete a;
-            return hip_fail(ctx, e, "hipMalloc of the arenas");
+            return fail(ctx, BL_ERR_HIP, "hipMalloc of %llu bytes of arenas", (unsigned long long)total);
         }
-        ctx->allocations++;
-        a->base = (char *)p;
     }
     bl_ctx_retain(ctx);
     *out = a;
@@ -254,7 +260,7 @@ static void arenas_free(bl_arenas *a) {
     if (a->base) {
         hipSetDevice(a->ctx->device);
         hipStreamSynchronize(a->ctx->stream);
-        hipFree(a->base);
+        bl_device_free(a->ctx, a->base, a->total);
     }
     bl_ctx *ctx = a->ctx;
     delete a;
@@ -544,6 +550,8 @@ struct bl_kernels {
     bl_arenas *arenas = nullptr;
     std::vector<Kernel> kernels;
     uint32_t sets = 1;
+    char *workspace = nullptr;  // the one allocation holding the three below
+    uint64_t workspace_bytes = 0;
     void *scratch = nullptr;
     float *partials = nullptr;  // split-k GEMMs' partial sums, shared as the attention scratch is
     std::vector<Pack> packs;
@@ -687,6 +695,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     std::vector<std::pair<size_t, size_t>> split_users;  // (kernel, set) of split-k GEMMs
 
     auto bad = [&](int code, const char *fmt, auto... args) {
+        bl_device_free(ctx, ks->workspace, ks->workspace_bytes);
         delete ks;
         return fail(ctx, code, fmt, args...);
     };
@@ -1080,22 +1089,34 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
         }
         ks->kernels.push_back(std::move(k));
     }
-    if (!ks->packs.empty()) {
-        uint64_t total = 0;
-        for (Pack &pk : ks->packs) {
-            pk.dst_offset = total;
-            total += (packed_bytes(pk.math, pk.k_pad, pk.n_pad) + 255) / 256 * 256;
-            // Written by a kernel of this program: packed again before every launch.
-            for (uint32_t ki = 0; ki < n && !pk.dynamic; ki++) {
-                const bl_binding &o = specs[ki].bindings[specs[ki].n_bindings - 1];
-                if (o.arena == pk.arena && o.offset < pk.offset + pk.size && pk.offset < o.offset + o.size)
-                    pk.dynamic = true;
-            }
+    // The backend's own device memory, one allocation beside the plan's
+    // arenas: the packed weights, then the split-k GEMMs' partial sums, then
+    // the attention scratch, each 256-byte aligned.
+    auto align256 = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    uint64_t pack_total = 0;
+    for (Pack &pk : ks->packs) {
+        pk.dst_offset = pack_total;
+        pack_total += align256(packed_bytes(pk.math, pk.k_pad, pk.n_pad));
+        // Written by a kernel of this program: packed again before every launch.
+        for (uint32_t ki = 0; ki < n && !pk.dynamic; ki++) {
+            const bl_binding &o = specs[ki].bindings[specs[ki].n_bindings - 1];
+            if (o.arena == pk.arena && o.offset < pk.offset + pk.size && pk.offset < o.offset + o.size)
+                pk.dynamic = true;
         }
-        for (const Pack &pk : ks->packs)
-            if (pk.dynamic) ks->graphs_ok = false;
-        ks->pack_buffer = bl_device_alloc(ctx, total);
-        if (!ks->pack_buffer) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of packed weights", (unsigned long long)total);
+    }
+    for (const Pack &pk : ks->packs)
+        if (pk.dynamic) ks->graphs_ok = false;
+    const uint64_t partial_at = pack_total, scratch_at = partial_at + align256(partial_bytes);
+    const uint64_t workspace = scratch_at + align256(scratch_bytes);
+    if (workspace) {
+        ks->workspace = (char *)bl_device_alloc(ctx, workspace);
+        if (!ks->workspace)
+            return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of workspace (packed weights, partial sums, attention scratch)",
+                       (unsigned long long)workspace);
+        ks->workspace_bytes = workspace;
+    }
+    if (pack_total) {
+        ks->pack_buffer = ks->workspace;
         for (Kernel &k : ks->kernels)
             for (Launch &L : k.per_set)
                 if (L.pack >= 0) L.gemm.b = (char *)ks->pack_buffer + ks->packs[L.pack].dst_offset;
@@ -1103,13 +1124,11 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     if (partial_bytes) {
         // Split-k GEMMs run one after another on the stream: one buffer serves
         // them all, every element written by its split before the reduce reads it.
-        ks->partials = (float *)bl_device_alloc(ctx, partial_bytes);
-        if (!ks->partials) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of split-k partial sums", (unsigned long long)partial_bytes);
+        ks->partials = (float *)(ks->workspace + partial_at);
         for (auto [ki, si] : split_users) ks->kernels[ki].per_set[si].gemm.partials = ks->partials;
     }
     if (scratch_bytes) {
-        ks->scratch = bl_device_alloc(ctx, scratch_bytes);
-        if (!ks->scratch) return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
+        ks->scratch = ks->workspace + scratch_at;
         // Kernels run one after another on the stream, so every flash kernel
         // uses the same scratch: operands, then partial outputs and statistics.
         for (auto [ki, si] : flash_users)
@@ -1164,9 +1183,7 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
     hipSetDevice(k->ctx->device);
     hipStreamSynchronize(k->ctx->stream);
     for (RangeGraph &g : k->graphs) hipGraphExecDestroy(g.exec);
-    if (k->scratch) hipFree(k->scratch);
-    if (k->partials) hipFree(k->partials);
-    if (k->pack_buffer) hipFree(k->pack_buffer);
+    bl_device_free(k->ctx, k->workspace, k->workspace_bytes);
     bl_ctx *ctx = k->ctx;
     bl_arenas *a = k->arenas;
     a->users.erase(std::find(a->users.begin(), a->users.end(), k));
@@ -1177,6 +1194,7 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
 }
 
 extern "C" uint64_t bl_kernels_packs_made(const bl_kernels *k) { return k ? k->packs_made : 0; }
+extern "C" uint64_t bl_kernels_workspace_bytes(const bl_kernels *k) { return k ? k->workspace_bytes : 0; }
 
 extern "C" uint32_t bl_kernels_len(const bl_kernels *k) { return k ? (uint32_t)k->kernels.size() : 0; }
 extern "C" uint32_t bl_kernels_sets(const bl_kernels *k) { return k ? k->sets : 0; }

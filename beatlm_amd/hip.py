@@ -173,6 +173,7 @@ _SIGNATURES = {
     "bl_ctx_set_f32_math": (C.c_int, [_VP, C.c_uint32]),
     "bl_ctx_synchronize": (C.c_int, [_VP]),
     "bl_ctx_allocations": (C.c_uint64, [_VP]),
+    "bl_ctx_device_bytes": (C.c_uint64, [_VP]),
     "bl_ctx_stream": (_VP, [_VP]),
     "bl_arenas_create": (C.c_int, [_VP, C.POINTER(C.c_uint64), C.c_uint32, C.POINTER(_VP)]),
     "bl_arenas_destroy": (None, [_VP]),
@@ -207,6 +208,7 @@ _SIGNATURES = {
     "bl_timer_stats": (C.c_int, [_VP, C.POINTER(TimerStats)]),
     "bl_kernels_time": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_float)]),
     "bl_kernels_packs_made": (C.c_uint64, [_VP]),
+    "bl_kernels_workspace_bytes": (C.c_uint64, [_VP]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
     "bl_flash_attention_static": (C.c_int, [_VP, _VP, _VP, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]),
 }
@@ -267,6 +269,10 @@ class Context:
 
     def allocations(self) -> int:
         return int(self._lib.bl_ctx_allocations(self.handle))
+
+    def device_bytes(self) -> int:
+        """Device bytes held now by this context's arenas and kernels."""
+        return int(self._lib.bl_ctx_device_bytes(self.handle))
 
     def spin(self, micros: int) -> None:
         self.check(self._lib.bl_spin(self.handle, micros))
@@ -378,6 +384,10 @@ class Kernels:
 
     def encode_all(self, set_index: int = 0) -> None:
         self.ctx.check(self.ctx._lib.bl_kernels_encode_range(self.handle, 0, len(self), set_index))
+
+    def workspace_bytes(self) -> int:
+        """Device bytes the kernels hold beside the arenas (one allocation)."""
+        return int(self.ctx._lib.bl_kernels_workspace_bytes(self.handle))
 
     def packs_made(self) -> int:
         return int(self.ctx._lib.bl_kernels_packs_made(self.handle))

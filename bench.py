@@ -589,7 +589,12 @@ def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_m
     elt = 2 if dtype == hip.F16 else 4
     frames = cfg["frames"]
     g, emb, block_ids, tokens = build_encoder(cfg)
+    allocs0, bytes0 = ctx.allocations(), ctx.device_bytes()
     prep = ir.prepare(ctx, g, dtype=dtype, slots=frames)
+    device_memory = {
+        "allocations": ctx.allocations() - allocs0, "bytes": ctx.device_bytes() - bytes0,
+        "arena_bytes": prep.plan.total_bytes(), "workspace_bytes": prep.kernels.workspace_bytes(),
+    }
     vals = synthetic_values(cfg, emb, block_ids, tokens, np_dtype)
     for tid, v in vals.items():
         prep.write(tid, v)
@@ -634,7 +639,7 @@ def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_m
                     f"(one job slot each), {cfg['dtype']}",
         "tokens": tokens, "blocks": cfg["blocks"], "frames": frames, "dtype": cfg["dtype"], "matrix_math": math_name,
         "value": round(us_per_block, 2), "unit": "us/block", "ms_per_step": round(ms_per_step, 4),
-        "kernels_per_frame": n_kernels,
+        "kernels_per_frame": n_kernels, "device_memory": device_memory,
         "per_kernel_us": {g: round(statistics.mean(per_launch[k] for k in ks), 2) for g, ks in groups.items()},
         "kernel_sum_us_per_block": round(sum(per_launch) / cfg["blocks"], 2),
     }

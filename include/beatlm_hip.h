@@ -219,6 +219,10 @@ int bl_ctx_synchronize(bl_ctx *ctx);
 /* Device allocations the context has made (arenas, scratch, events): the
  * frame loop's count must not move. */
 uint64_t bl_ctx_allocations(const bl_ctx *ctx);
+/* Bytes of device memory the context's live arenas and kernels hold now: the
+ * arenas' one allocation each plus each kernels' workspace
+ * (bl_kernels_workspace_bytes). No counterpart in the reference. */
+uint64_t bl_ctx_device_bytes(const bl_ctx *ctx);
 /* The context's HIP stream (hipStream_t), for hosts that order their own work
  * (e.g. a render pass) on it. */
 void *bl_ctx_stream(bl_ctx *ctx);
@@ -305,6 +309,12 @@ int bl_kernels_time(bl_kernels *kernels, uint32_t kernel, uint32_t set, uint32_t
  * counterpart in the reference: lets a host check its frame loop repacks
  * nothing. */
 uint64_t bl_kernels_packs_made(const bl_kernels *kernels);
+/* Bytes of device memory the kernels hold beside the plan's arenas, in one
+ * allocation made by bl_kernels_create (0: none): packed weights, split-k
+ * partial sums, attention scratch. No counterpart in the reference, whose
+ * kernels hold no memory of their own; with the arenas' one allocation, a
+ * program's device memory is these two allocations. */
+uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
 
 /* ---- flash attention that allocates nothing ----
  * No counterpart in the reference. For callers that cannot allocate device

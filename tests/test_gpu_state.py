@@ -203,3 +203,37 @@ def test_kernels_keep_their_arenas(ctx):
     rt.hipMemGetInfo(C.byref(free1), C.byref(total))
     # Everything the program allocated is back (within allocator granularity).
     assert free1.value + (64 << 20) >= free0.value
+
+
+def test_a_program_holds_two_allocations_that_do_not_move_over_100_frames(ctx):
+    """The arenas are one allocation and the kernels' workspace (packed
+    weights, split-k partials, attention scratch) another; the device bytes
+    held are exactly the plan's arenas plus that workspace; 100 frames with a
+    new input each allocate nothing and hold no more."""
+    t, d, h, mlp = 1370, 384, 6, 1536
+    w = block_weights(d, mlp, 301, "xavier")
+    g, ids = block_graph(t, d, h, mlp, EPS)
+    allocs0, bytes0 = ctx.allocations(), ctx.device_bytes()
+    prep = ir.prepare(ctx, g)
+    assert ctx.allocations() == allocs0 + 2, "arenas + workspace"
+    ws = prep.kernels.workspace_bytes()
+    assert ws > 0
+    arenas = 0
+    for size in prep.plan.arenas():
+        arenas = (arenas + 255) // 256 * 256 + size
+    assert ctx.device_bytes() == bytes0 + arenas + ws
+    for tid, v in block_values(ids, oracle.normal(8, t * d), w).items():
+        prep.write(tid, v)
+    prep.run()
+    ctx.synchronize()
+    held = ctx.allocations(), ctx.device_bytes()
+    for frame in range(100):
+        if frame % 10 == 0:
+            prep.write(0, oracle.normal(500 + frame, t * d))
+        prep.run()
+    ctx.synchronize()
+    assert (ctx.allocations(), ctx.device_bytes()) == held
+    x = oracle.normal(590, t * d)
+    assert_close(prep.read(ids.output), oracle.vit_block(x, w, t, h, d // h, mlp, EPS), "after 100 frames")
+    prep.close()
+    assert ctx.device_bytes() == bytes0
