@@ -43,6 +43,7 @@ SOURCES = [
     "static_attention.hip",
     "backend.cpp",
     "timer.cpp",
+    "ring.cpp",
     "ir.cpp",
     "cost.cpp",
     "schedule.cpp",

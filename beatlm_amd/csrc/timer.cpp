@@ -1,33 +1,34 @@
 // The slice timer: per-slice GPU durations from hipEvent pairs, read back
 // without ever blocking. The HIP counterpart of the reference's SliceTimer
-// (crates/beatlm/src/gpu/timer.rs:185-464) and its ring
-// (crates/beatlm/src/gpu/ring.rs):
+// (crates/beatlm/src/gpu/timer.rs:185-464); which slot a frame uses and when
+// its events may be read is the ring's bookkeeping (ring.hpp), and this file
+// holds only the events:
 //
-//  - a ring of BL_TIMER_RING_DEPTH frames in flight, each with an event pair
-//    per slice and one event closing the frame, all created once;
+//  - BL_TIMER_RING_DEPTH slots, each with an event pair per slice, a pair for
+//    the render pass and one event closing the frame, all created once;
 //  - a frame whose slot is still in flight when it begins is not timed, and
 //    is counted skipped; nothing waits;
-//  - only frames the host hands back as submitted are read, in submission
-//    order; a resolved frame never handed back frees its slot unread;
+//  - a resolved frame is read only once the host hands its ticket back as
+//    submitted, frames come back in submission order, and a ticket given up
+//    (bl_timer_abandon) frees its slot unread;
+//  - held frames are read only once the host's verdict accepts them;
 //  - frames the host marks (bl_timer_invalidate_submitted) are never
-//    decoded: they free their slot and count as failed;
-//  - completion is polled with hipEventQuery, so collecting never blocks.
+//    decoded: they free their slot once their events completed and count as
+//    failed;
+//  - a slot's work stands where hipEventQuery of its closing event says, so
+//    collecting never blocks.
 #include <hip/hip_runtime.h>
 
-#include <deque>
 #include <string>
 #include <vector>
 
+#include "ring.hpp"
 #include "timer.hpp"
 #include "../../include/beatlm_schedule.h"
 
 namespace {
 
-enum class State { FREE, RECORDING, RESOLVED, SUBMITTED };
-
 struct Slot {
-    State state = State::FREE;
-    bool invalid = false;
     uint64_t frame = 0;
     uint32_t used = 0;
     std::vector<hipEvent_t> events;  // 2 per slice
@@ -43,11 +44,11 @@ struct bl_timer {
     bl_ctx *ctx = nullptr;
     bool retained = false;         // holds a reference on ctx (set once created)
     uint32_t max_slices = 0;
+    bl::Ring ring{BL_TIMER_RING_DEPTH};
     std::vector<Slot> slots;
     int open = -1;                 // slot of the frame being recorded, -1 when untimed
     bool frame_open = false;
     bool render_begun = false;     // the open frame's render pass was requested
-    std::deque<int> submitted;     // submission order
     bl_timer_stats_t stats{};
     // What the last collect returned; valid until the next collect.
     std::vector<std::vector<uint32_t>> out_tags;
@@ -108,29 +109,21 @@ extern "C" void bl_timer_destroy(bl_timer *t) {
 
 extern "C" int bl_timer_begin_frame(bl_timer *t, uint64_t frame, uint32_t *timed) {
     if (!t) return BL_ERR_INVALID_ARGUMENT;
-    // A frame still open, or resolved and never handed back, is dropped unread.
-    for (Slot &s : t->slots) {
-        if (s.state == State::RECORDING || s.state == State::RESOLVED) {
-            s.state = State::FREE;
-            t->stats.frames_dropped++;
-        }
+    // A frame still open (begun, never resolved) gives its slot back unread.
+    if (t->frame_open && t->open >= 0) {
+        t->ring.release((uint32_t)t->open);
+        t->stats.frames_dropped++;
     }
+    const uint64_t reclaimed = t->ring.reclaimed();
+    t->open = t->ring.claim();
+    t->stats.frames_dropped += t->ring.reclaimed() - reclaimed;  // tickets given up
     t->stats.frames_begun++;
     t->frame_open = true;
     t->render_begun = false;
-    t->open = -1;
-    for (size_t i = 0; i < t->slots.size(); i++) {
-        if (t->slots[i].state == State::FREE) {
-            t->open = (int)i;
-            break;
-        }
-    }
     if (t->open < 0) {
         t->stats.frames_skipped++;
     } else {
         Slot &s = t->slots[t->open];
-        s.state = State::RECORDING;
-        s.invalid = false;
         s.frame = frame;
         s.used = 0;
         s.render_state = 0;
@@ -186,31 +179,76 @@ extern "C" int bl_timer_render_end(bl_timer *t) {
     return BL_OK;
 }
 
-extern "C" int bl_timer_resolve(bl_timer *t, uint32_t *resolved) {
+extern "C" int bl_timer_resolve(bl_timer *t, uint64_t *resolved) {
     if (!t || !resolved) return BL_ERR_INVALID_ARGUMENT;
+    *resolved = 0;  // untimed: handing it back is accepted and ignored
     if (!t->frame_open) return bl_fail(t->ctx, BL_ERR_TIMER_NO_FRAME, "no frame is open on the timer");
     t->frame_open = false;
-    if (t->open < 0) {
-        *resolved = UINT32_MAX;  // untimed: handing it back is accepted and ignored
-        return BL_OK;
-    }
-    Slot &s = t->slots[t->open];
-    if (hipEventRecord(s.done, bl_stream_of(t->ctx)) != hipSuccess)
-        return bl_fail(t->ctx, BL_ERR_HIP, "hipEventRecord");
-    s.state = State::RESOLVED;
-    *resolved = (uint32_t)t->open;
+    if (t->open < 0) return BL_OK;
+    const uint32_t i = (uint32_t)t->open;
     t->open = -1;
+    if (hipEventRecord(t->slots[i].done, bl_stream_of(t->ctx)) != hipSuccess) {
+        t->ring.release(i);
+        return bl_fail(t->ctx, BL_ERR_HIP, "hipEventRecord");
+    }
+    *resolved = t->ring.encode(i);
     return BL_OK;
 }
 
-extern "C" int bl_timer_submitted(bl_timer *t, uint32_t resolved) {
+extern "C" int bl_timer_submitted(bl_timer *t, uint64_t resolved) {
     if (!t) return BL_ERR_INVALID_ARGUMENT;
-    if (resolved >= t->slots.size()) return BL_OK;
-    Slot &s = t->slots[resolved];
-    if (s.state != State::RESOLVED) return BL_OK;
-    s.state = State::SUBMITTED;
-    t->submitted.push_back((int)resolved);
+    if (resolved) t->ring.submit(resolved);  // another timer's frame goes untimed
     return BL_OK;
+}
+
+extern "C" int bl_timer_submitted_held(bl_timer *t, uint64_t resolved, uint64_t *hold) {
+    if (!t || !hold) return BL_ERR_INVALID_ARGUMENT;
+    *hold = 0;
+    if (resolved) t->ring.submit_held(resolved, hold);
+    return BL_OK;
+}
+
+extern "C" int bl_timer_verdict(bl_timer *t, uint64_t hold, uint32_t accepted) {
+    if (!t) return BL_ERR_INVALID_ARGUMENT;
+    return hold && bl::give_verdict(hold, accepted != 0) ? 1 : 0;
+}
+
+extern "C" int bl_timer_abandon(bl_timer *t, uint64_t resolved) {
+    if (!t) return BL_ERR_INVALID_ARGUMENT;
+    if (resolved) bl::drop_ticket(resolved);
+    return BL_OK;
+}
+
+extern "C" uint32_t bl_timer_in_flight(const bl_timer *t) { return t ? t->ring.in_flight() : 0; }
+
+// Reads slot `i`'s slice and render durations into out[*n_out]; false when
+// an elapsed time cannot be read.
+static bool read_slot(bl_timer *t, uint32_t i, bl_frame_timing *out, uint32_t *n_out) {
+    Slot &s = t->slots[i];
+    std::vector<uint32_t> tags(s.tags.begin(), s.tags.begin() + s.used);
+    std::vector<float> micros(s.used, 0.0f);
+    for (uint32_t j = 0; j < s.used; j++) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, s.events[2 * j], s.events[2 * j + 1]) != hipSuccess) return false;
+        micros[j] = ms * 1000.0f;
+    }
+    t->out_tags.push_back(std::move(tags));
+    t->out_micros.push_back(std::move(micros));
+    bl_frame_timing &f = out[*n_out];
+    f.frame = s.frame;
+    f.n_slices = s.used;
+    f.failed = 0;
+    f.tags = t->out_tags.back().data();
+    f.micros = t->out_micros.back().data();
+    f.has_render = 0;
+    f.render_micros = 0.0f;
+    float ms = 0.0f;
+    if (s.render_state == 2 && hipEventElapsedTime(&ms, s.render[0], s.render[1]) == hipSuccess) {
+        f.has_render = 1;
+        f.render_micros = ms * 1000.0f;
+    }
+    (*n_out)++;
+    return true;
 }
 
 extern "C" int bl_timer_collect(bl_timer *t, bl_frame_timing *out, uint32_t cap, uint32_t *n_out) {
@@ -220,55 +258,32 @@ extern "C" int bl_timer_collect(bl_timer *t, bl_frame_timing *out, uint32_t cap,
     t->out_micros.clear();
     t->out_tags.reserve(cap);
     t->out_micros.reserve(cap);
-    while (!t->submitted.empty()) {
-        Slot &s = t->slots[t->submitted.front()];
-        hipError_t q = hipEventQuery(s.done);
-        if (q == hipErrorNotReady) break;  // later frames wait: submission order
-        bool ok = q == hipSuccess && !s.invalid;
-        if (ok && *n_out >= cap) break;   // no room: leave it for the next call
-        if (ok) {
-            std::vector<uint32_t> tags(s.tags.begin(), s.tags.begin() + s.used);
-            std::vector<float> micros(s.used, 0.0f);
-            for (uint32_t i = 0; i < s.used && ok; i++) {
-                float ms = 0.0f;
-                if (hipEventElapsedTime(&ms, s.events[2 * i], s.events[2 * i + 1]) != hipSuccess) ok = false;
-                micros[i] = ms * 1000.0f;
-            }
-            if (ok) {
-                t->out_tags.push_back(std::move(tags));
-                t->out_micros.push_back(std::move(micros));
-                bl_frame_timing &f = out[*n_out];
-                f.frame = s.frame;
-                f.n_slices = s.used;
-                f.failed = 0;
-                f.tags = t->out_tags.back().data();
-                f.micros = t->out_micros.back().data();
-                f.has_render = 0;
-                f.render_micros = 0.0f;
-                float ms = 0.0f;
-                if (s.render_state == 2 && hipEventElapsedTime(&ms, s.render[0], s.render[1]) == hipSuccess) {
-                    f.has_render = 1;
-                    f.render_micros = ms * 1000.0f;
-                }
-                (*n_out)++;
-                t->stats.frames_timed++;
-            }
+    t->ring.settle();
+    uint32_t slots[bl::RING_MAX_DEPTH];
+    bl::Action actions[bl::RING_MAX_DEPTH];
+    const uint32_t n = t->ring.ready(
+        [t](uint32_t i) {
+            const hipError_t q = hipEventQuery(t->slots[i].done);
+            return q == hipSuccess ? bl::Done::OK : q == hipErrorNotReady ? bl::Done::PENDING : bl::Done::FAILED;
+        },
+        slots, actions);
+    for (uint32_t j = 0; j < n; j++) {
+        const uint32_t i = slots[j];
+        if (actions[j] == bl::Action::READ) {
+            if (*n_out >= cap) break;  // no room: it and what follows wait for the next call
+            if (read_slot(t, i, out, n_out)) t->stats.frames_timed++;
+            else t->stats.frames_failed++;
+        } else {
+            t->stats.frames_failed++;
         }
-        if (!ok) t->stats.frames_failed++;
-        s.state = State::FREE;
-        t->submitted.pop_front();
+        t->ring.release(i);
     }
     return BL_OK;
 }
 
 extern "C" int bl_timer_invalidate_submitted(bl_timer *t) {
     if (!t) return BL_ERR_INVALID_ARGUMENT;
-    int marked = 0;
-    for (int i : t->submitted) {
-        if (!t->slots[i].invalid) marked++;
-        t->slots[i].invalid = true;
-    }
-    return marked;
+    return (int)t->ring.invalidate();
 }
 
 extern "C" int bl_timer_stats(const bl_timer *t, bl_timer_stats_t *out) {

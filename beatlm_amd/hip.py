@@ -199,10 +199,14 @@ _SIGNATURES = {
     "bl_timer_create": (C.c_int, [_VP, C.c_uint32, C.POINTER(_VP)]),
     "bl_timer_destroy": (None, [_VP]),
     "bl_timer_begin_frame": (C.c_int, [_VP, C.c_uint64, C.POINTER(C.c_uint32)]),
-    "bl_timer_resolve": (C.c_int, [_VP, C.POINTER(C.c_uint32)]),
+    "bl_timer_resolve": (C.c_int, [_VP, C.POINTER(C.c_uint64)]),
     "bl_timer_render_begin": (C.c_int, [_VP]),
     "bl_timer_render_end": (C.c_int, [_VP]),
-    "bl_timer_submitted": (C.c_int, [_VP, C.c_uint32]),
+    "bl_timer_submitted": (C.c_int, [_VP, C.c_uint64]),
+    "bl_timer_submitted_held": (C.c_int, [_VP, C.c_uint64, C.POINTER(C.c_uint64)]),
+    "bl_timer_verdict": (C.c_int, [_VP, C.c_uint64, C.c_uint32]),
+    "bl_timer_abandon": (C.c_int, [_VP, C.c_uint64]),
+    "bl_timer_in_flight": (C.c_uint32, [_VP]),
     "bl_timer_collect": (C.c_int, [_VP, C.POINTER(FrameTiming), C.c_uint32, C.POINTER(C.c_uint32)]),
     "bl_timer_invalidate_submitted": (C.c_int, [_VP]),
     "bl_timer_stats": (C.c_int, [_VP, C.POINTER(TimerStats)]),
@@ -425,12 +429,30 @@ class Timer:
         return bool(timed.value)
 
     def resolve(self) -> int:
-        r = C.c_uint32()
+        """Closes the open frame; returns its ticket (0: untimed)."""
+        r = C.c_uint64()
         self.ctx.check(self.ctx._lib.bl_timer_resolve(self.handle, C.byref(r)))
         return r.value
 
     def submitted(self, resolved: int) -> None:
         self.ctx.check(self.ctx._lib.bl_timer_submitted(self.handle, resolved))
+
+    def submitted_held(self, resolved: int) -> int:
+        """Hands the ticket back held; returns the hold for verdict() (0: nothing held)."""
+        h = C.c_uint64()
+        self.ctx.check(self.ctx._lib.bl_timer_submitted_held(self.handle, resolved, C.byref(h)))
+        return h.value
+
+    def verdict(self, hold: int, accepted: bool) -> bool:
+        """HeldFrame::accept / reject; False when the frame had moved on."""
+        return self.ctx.check(self.ctx._lib.bl_timer_verdict(self.handle, hold, 1 if accepted else 0)) == 1
+
+    def abandon(self, resolved: int) -> None:
+        """The frame's work was never submitted: its slot is freed unread."""
+        self.ctx.check(self.ctx._lib.bl_timer_abandon(self.handle, resolved))
+
+    def in_flight(self) -> int:
+        return int(self.ctx._lib.bl_timer_in_flight(self.handle))
 
     def render_begin(self) -> None:
         self.ctx.check(self.ctx._lib.bl_timer_render_begin(self.handle))

@@ -248,6 +248,23 @@ _SIG = {
     "bls_step_absorb": (_I, [_VP, C.POINTER(_FrameTiming), C.POINTER(_Absorbed)]),
     "bls_step_complete": (_I, [_VP, _U64, C.POINTER(_Plan)]),
     "bls_step_finish": (_I, [_VP, C.POINTER(_Tally)]),
+    "bls_collect_action": (_U32, [_U32, _U32]),
+    "bls_ring_new": (_I, [_U32, C.POINTER(_VP)]),
+    "bls_ring_free": (None, [_VP]),
+    "bls_ring_depth": (_U32, [_VP]),
+    "bls_ring_claim": (C.c_int32, [_VP]),
+    "bls_ring_encode": (_U64, [_VP, _U32]),
+    "bls_ring_submit": (C.c_int32, [_VP, _U64]),
+    "bls_ring_submit_held": (C.c_int32, [_VP, _U64, _P64]),
+    "bls_ticket_drop": (None, [_U64]),
+    "bls_hold_verdict": (_I, [_U64, _U32]),
+    "bls_ring_settle": (None, [_VP]),
+    "bls_ring_invalidate": (_U32, [_VP]),
+    "bls_ring_ready": (_U32, [_VP, C.POINTER(C.c_uint8), _PU32, C.POINTER(C.c_uint8)]),
+    "bls_ring_release": (None, [_VP, _U32]),
+    "bls_ring_in_flight": (_U32, [_VP]),
+    "bls_ring_phase": (C.c_int32, [_VP, _U32]),
+    "bls_ring_reclaimed": (_U64, [_VP]),
 }
 _bound = False
 
@@ -759,3 +776,99 @@ class FrameStep:
         if getattr(self, "handle", None):
             _lib().bls_step_free(self.handle)
             self.handle = None
+
+
+# ---- the slice timer's ring (crates/beatlm/src/gpu/ring.rs) ------------------
+
+PHASE_FREE, PHASE_RECORDING, PHASE_ENCODED, PHASE_SUBMITTED, PHASE_HELD, PHASE_INVALID = range(6)
+DONE_PENDING, DONE_OK, DONE_FAILED = range(3)
+COLLECT_WAIT, COLLECT_READ, COLLECT_DROP = range(3)
+RING_MAX_DEPTH = 64
+
+
+def collect_action(phase: int, done: int) -> int:
+    """`collect` (ring.rs:98-111): what collecting a slot does now."""
+    return int(_lib().bls_collect_action(phase, done))
+
+
+def drop_ticket(ticket: int) -> None:
+    """Dropping a `Ticket`: its slot is freed unread at its ring's next claim."""
+    _lib().bls_ticket_drop(ticket)
+
+
+def verdict(hold: int, accepted: bool) -> bool:
+    """`Verdict::accept` / `reject`; False when it reached no held slot."""
+    return bool(_lib().bls_hold_verdict(hold, 1 if accepted else 0))
+
+
+class Ring:
+    """`Ring` (ring.rs:184-412). Tickets and holds are ints (never 0); a
+    method that gives None where the reference gives None."""
+
+    def __init__(self, depth: int):
+        h = _VP()
+        _check(_lib().bls_ring_new(depth, C.byref(h)))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            _lib().bls_ring_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def depth(self) -> int:
+        return int(_lib().bls_ring_depth(self.handle))
+
+    def claim(self) -> int | None:
+        s = _lib().bls_ring_claim(self.handle)
+        return None if s < 0 else int(s)
+
+    def encode(self, slot: int) -> int | None:
+        t = _lib().bls_ring_encode(self.handle, slot)
+        return None if t == 0 else int(t)
+
+    def submit(self, ticket: int) -> int | None:
+        s = _lib().bls_ring_submit(self.handle, ticket)
+        return None if s < 0 else int(s)
+
+    def submit_held(self, ticket: int) -> tuple[int, int] | None:
+        h = C.c_uint64()
+        s = _lib().bls_ring_submit_held(self.handle, ticket, C.byref(h))
+        return None if s < 0 else (int(s), int(h.value))
+
+    def settle(self) -> None:
+        _lib().bls_ring_settle(self.handle)
+
+    def invalidate(self) -> int:
+        return int(_lib().bls_ring_invalidate(self.handle))
+
+    def ready(self, done) -> list[tuple[int, int]]:
+        """(slot, COLLECT_*) pairs to collect now, oldest submission first;
+        `done(slot)` gives DONE_* for each slot."""
+        n = self.depth()
+        d = (C.c_uint8 * n)(*[done(i) for i in range(n)])
+        slots = (C.c_uint32 * n)()
+        acts = (C.c_uint8 * n)()
+        k = _lib().bls_ring_ready(self.handle, d, slots, acts)
+        return [(int(slots[i]), int(acts[i])) for i in range(k)]
+
+    def release(self, slot: int) -> None:
+        _lib().bls_ring_release(self.handle, slot)
+
+    def in_flight(self) -> int:
+        return int(_lib().bls_ring_in_flight(self.handle))
+
+    def phase(self, slot: int) -> int | None:
+        p = _lib().bls_ring_phase(self.handle, slot)
+        return None if p < 0 else int(p)
+
+    def slots_in(self, phase: int) -> list[int]:
+        return [i for i in range(self.depth()) if self.phase(i) == phase]
+
+    def reclaimed(self) -> int:
+        return int(_lib().bls_ring_reclaimed(self.handle))

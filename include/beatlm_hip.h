@@ -20,6 +20,10 @@
  *   FrameTimestamps::compute_pass(tag)  gpu/timer.rs:507    (timer argument of bl_kernels_encode)
  *   FrameTimestamps::resolve(encoder)   gpu/timer.rs:561    bl_timer_resolve
  *   SliceTimer::submitted(resolved)     gpu/timer.rs:307    bl_timer_submitted
+ *   SliceTimer::submitted_held(resolved) gpu/timer.rs:332   bl_timer_submitted_held
+ *   HeldFrame::accept / reject          gpu/timer.rs:674-684 bl_timer_verdict
+ *   drop(ResolvedFrame)                 gpu/ring.rs:113-140 bl_timer_abandon
+ *   SliceTimer::in_flight()             gpu/timer.rs:452    bl_timer_in_flight
  *   SliceTimer::collect_ready()         gpu/timer.rs:371    bl_timer_collect
  *   SliceTimer::invalidate_submitted()  gpu/timer.rs:445    bl_timer_invalidate_submitted
  *   SliceTimer::stats()                 gpu/timer.rs:458    bl_timer_stats
@@ -47,7 +51,7 @@
 extern "C" {
 #endif
 
-#define BL_ABI_VERSION 3u
+#define BL_ABI_VERSION 4u
 #define BL_MAX_EPILOGUE 8
 #define BL_MAX_BINDINGS 8
 
@@ -362,16 +366,39 @@ int bl_timer_begin_frame(bl_timer *timer, uint64_t frame, uint32_t *timed);
  * nothing is recorded when the frame is untimed). */
 int bl_timer_render_begin(bl_timer *timer);
 int bl_timer_render_end(bl_timer *timer);
-/* Closes the open frame; `*resolved` names it for bl_timer_submitted. */
-int bl_timer_resolve(bl_timer *timer, uint32_t *resolved);
-/* The host says the frame's work reached the stream. A resolved frame never
- * submitted is dropped by the next begin_frame, unread. */
-int bl_timer_submitted(bl_timer *timer, uint32_t resolved);
-/* The frames whose events have all completed, in submission order, without
- * blocking (hipEventQuery). Fills up to `cap` entries. */
+/* Closes the open frame. `*resolved` is its ticket (0 for an untimed frame),
+ * spent by exactly one of bl_timer_submitted, bl_timer_submitted_held or
+ * bl_timer_abandon; until then the frame keeps its slot, and tickets may come
+ * back in any order. A frame begun while another is open drops the open one
+ * unread (frames_dropped). */
+int bl_timer_resolve(bl_timer *timer, uint64_t *resolved);
+/* The host says the frame's work reached the stream: only now may it be read.
+ * A ticket of 0, from another timer or an earlier lap is accepted and ignored
+ * (another timer's frame then goes untimed). */
+int bl_timer_submitted(bl_timer *timer, uint64_t resolved);
+/* bl_timer_submitted for a host that learns later whether the submission
+ * ran: the frame is read only once bl_timer_verdict accepts `*hold` (0 when
+ * there is nothing to hold), and frames submitted after it wait for it. */
+int bl_timer_submitted_held(bl_timer *timer, uint64_t resolved, uint64_t *hold);
+/* The verdict on a held frame: accepted (read once its events completed) or
+ * rejected (dropped unread, holding back nothing). Returns 1 when it reached
+ * the frame, 0 when the frame had been invalidated meanwhile. A hold never
+ * given a verdict waits, and holds back every later frame, until
+ * bl_timer_invalidate_submitted. */
+int bl_timer_verdict(bl_timer *timer, uint64_t hold, uint32_t accepted);
+/* The frame's work was never submitted (an error path): its slot is freed
+ * unread at the next begin_frame and counted in frames_dropped. */
+int bl_timer_abandon(bl_timer *timer, uint64_t resolved);
+/* Frames recorded or submitted and not yet collected (an abandoned one is not). */
+uint32_t bl_timer_in_flight(const bl_timer *timer);
+/* The frames ready to read, in submission order, without blocking
+ * (hipEventQuery): a frame waits while one submitted before it is held or
+ * still running; invalid and failed frames are freed and hold back nothing.
+ * Fills up to `cap` entries. */
 int bl_timer_collect(bl_timer *timer, bl_frame_timing *out, uint32_t cap,
                      uint32_t *n_out);
-/* Every submitted frame not yet collected is marked failed (never decoded). */
+/* Every submitted or held frame not yet collected is marked failed: never
+ * decoded, freed once its events complete. Returns how many were marked. */
 int bl_timer_invalidate_submitted(bl_timer *timer);
 int bl_timer_stats(const bl_timer *timer, bl_timer_stats_t *out);
 

@@ -26,6 +26,12 @@
  *   frame.rs:163-240               Submit, Admission               BLS_SUBMIT_*, inside bls_step
  *   frame.rs:264-283               timer_capacity, jobs_with_slices bls_timer_capacity, bls_jobs_with_slices
  *   beatlm-host/src/step.rs:78-540 StepConfig, FrameStep, Tally    bls_step_*
+ *   beatlm/src/gpu/ring.rs:98-111  collect                         bls_collect_action
+ *   ring.rs:184-412                Ring (claim, encode, submit,    bls_ring_*
+ *                                  submit_held, settle, invalidate,
+ *                                  ready, release, in_flight)
+ *   ring.rs:113-182                Ticket / Verdict drop, accept,  bls_ticket_drop, bls_hold_verdict
+ *                                  reject
  *
  * Times are microseconds (Micros, TimePoint), frames are FrameIndex values.
  * Every call is deterministic. Handles are not thread-safe; one handle may
@@ -183,6 +189,72 @@ int bls_scheduler_plan_frame(bls_scheduler *s, const bls_frame *frame, uint64_t 
                              bls_frame_plan *out);
 uint32_t bls_scheduler_pending(const bls_scheduler *s);
 int bls_scheduler_due(const bls_scheduler *s, uint64_t job, bls_due *out);
+
+/* ---- the slice timer's ring (no GPU in it) ------------------------------- */
+/* Which ring slot a frame's timing uses and when it may be read; the HIP
+ * slice timer (bl_timer_*) runs one ring per timer. A slot goes FREE ->
+ * RECORDING (bls_ring_claim) -> ENCODED (bls_ring_encode hands out a ticket)
+ * -> SUBMITTED (the ticket came back through bls_ring_submit) or HELD
+ * (bls_ring_submit_held: read only once its verdict accepts it) -> FREE
+ * (bls_ring_release, once collected). INVALID: submitted or held, then marked
+ * by bls_ring_invalidate or rejected; freed unread once its work completes.
+ *
+ * Tickets and holds are nonzero 64-bit values naming the ring, the slot and
+ * the lap: one from an earlier lap is refused, and one handed to another ring
+ * is refused there and dropped in its own ring. A ticket is spent by exactly
+ * one of bls_ring_submit, bls_ring_submit_held or bls_ticket_drop; a ticket
+ * dropped frees its slot unread at the ring's next claim. A hold is spent by
+ * bls_hold_verdict (the C form of Verdict::accept / reject; a verdict never
+ * given keeps its slot, and every later read, waiting until the ring is
+ * invalidated). bls_ticket_drop and bls_hold_verdict may be called from any
+ * thread; a ring from one thread at a time. */
+typedef struct bls_ring bls_ring;
+enum { BLS_PHASE_FREE = 0, BLS_PHASE_RECORDING = 1, BLS_PHASE_ENCODED = 2, BLS_PHASE_SUBMITTED = 3,
+       BLS_PHASE_HELD = 4, BLS_PHASE_INVALID = 5 };
+/* Where a slot's work stands (its closing event: pending, completed, failed). */
+enum { BLS_DONE_PENDING = 0, BLS_DONE_OK = 1, BLS_DONE_FAILED = 2 };
+enum { BLS_COLLECT_WAIT = 0, BLS_COLLECT_READ = 1, BLS_COLLECT_DROP = 2 };
+#define BLS_RING_MAX_DEPTH 64
+
+/* collect (ring.rs:98-111): READ only SUBMITTED with its work completed;
+ * DROP an INVALID slot once its work completed or failed, and a SUBMITTED
+ * one whose work failed; WAIT otherwise (HELD always). */
+uint32_t bls_collect_action(uint32_t phase, uint32_t done);
+/* `depth` free slots (0 is raised to 1); BLS_ERR_INVALID above BLS_RING_MAX_DEPTH. */
+int bls_ring_new(uint32_t depth, bls_ring **out);
+void bls_ring_free(bls_ring *r);
+uint32_t bls_ring_depth(const bls_ring *r);
+/* Frees slots whose ticket was dropped, then takes the slot at the cursor if
+ * it is free and moves the cursor on; -1 when it is busy (the cursor stays). */
+int32_t bls_ring_claim(bls_ring *r);
+/* The RECORDING slot's frame is closed: its ticket, 0 if not recording. */
+uint64_t bls_ring_encode(bls_ring *r, uint32_t slot);
+/* The ticket comes back after its work was submitted: the slot, now
+ * SUBMITTED, or -1 (not this ring's, an earlier lap's, or dropped). */
+int32_t bls_ring_submit(bls_ring *r, uint64_t ticket);
+/* bls_ring_submit, but the slot is HELD; *hold names it for bls_hold_verdict. */
+int32_t bls_ring_submit_held(bls_ring *r, uint64_t ticket, uint64_t *hold);
+/* The frame's work was never submitted (or the host cannot tell). */
+void bls_ticket_drop(uint64_t ticket);
+/* 1 when the verdict reached its HELD slot; 0 when the slot moved on
+ * (invalidated, released, held again by a later frame) or the ring is gone.
+ * The slot moves at the ring's next bls_ring_settle. */
+int bls_hold_verdict(uint64_t hold, uint32_t accepted);
+void bls_ring_settle(bls_ring *r);
+/* Every SUBMITTED or HELD slot -> INVALID; returns how many moved. */
+uint32_t bls_ring_invalidate(bls_ring *r);
+/* The slots to collect now, oldest submission first, given `done[slot]`
+ * (BLS_DONE_*, one per slot of the ring): a READ waits while a slot
+ * submitted before it is HELD or SUBMITTED with its work pending; DROPs
+ * never wait. Writes up to depth entries to `slots` and `actions`. */
+uint32_t bls_ring_ready(const bls_ring *r, const uint8_t *done, uint32_t *slots, uint8_t *actions);
+void bls_ring_release(bls_ring *r, uint32_t slot);
+/* Slots neither FREE nor waiting on a dropped ticket. */
+uint32_t bls_ring_in_flight(const bls_ring *r);
+/* BLS_PHASE_*, -1 for a slot the ring does not have. */
+int32_t bls_ring_phase(const bls_ring *r, uint32_t slot);
+/* Slots freed so far because their ticket was dropped. */
+uint64_t bls_ring_reclaimed(const bls_ring *r);
 
 /* ---- the host's frame step ---------------------------------------------- */
 

@@ -32,7 +32,7 @@ def test_the_library_exports_every_declared_function():
 
 
 def test_the_abi_version():
-    assert hip.lib().bl_abi_version() == 3
+    assert hip.lib().bl_abi_version() == 4
 
 
 C_LAYOUT = r"""

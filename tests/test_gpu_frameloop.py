@@ -105,16 +105,120 @@ def test_invalidated_frames_are_never_decoded_and_count_as_failed(ctx, small):
         timer.close()
 
 
-def test_a_resolved_frame_never_handed_back_is_dropped(ctx, small):
+def run_frame(ctx, prep, timer, frame):
+    """One frame through the timer: encode, hand back, wait, collect."""
+    _, r = encode_frame(prep, timer, frame, tags=[1000 + frame] * len(prep.kernels))
+    timer.submitted(r)
+    ctx.synchronize()
+    return timer.collect()
+
+
+def test_an_abandoned_frame_is_never_read_and_its_slot_comes_back(ctx, small):
+    """gpu/timer.rs:964-1017: after a lap every slot's events hold real
+    times; a frame resolved and then given up (its work never handed back)
+    is not read, the next frame is reported as itself, and the freed slot
+    serves a further lap."""
     _, _, _, prep = small
     timer = hip.Timer(ctx, len(prep.kernels))
     try:
-        encode_frame(prep, timer, 0)  # resolved, never submitted
-        _, r = encode_frame(prep, timer, 1)
+        for f in range(hip.RING_DEPTH):
+            assert [x for x, _ in run_frame(ctx, prep, timer, f)] == [f]
+        dropped = hip.RING_DEPTH
+        _, r = encode_frame(prep, timer, dropped)
+        assert r != 0
+        timer.abandon(r)
+        assert timer.in_flight() == 0
+        timer.submitted(r)  # spent: handing it back afterwards is ignored
+        nxt = dropped + 1
+        got = run_frame(ctx, prep, timer, nxt)
+        assert [x for x, _ in got] == [nxt]
+        assert {t for t, _ in got[0][1]} == {1000 + nxt}
+        assert timer.in_flight() == 0
+        for f in range(nxt + 1, nxt + 1 + hip.RING_DEPTH):
+            got = run_frame(ctx, prep, timer, f)
+            assert [x for x, _ in got] == [f] and {t for t, _ in got[0][1]} == {1000 + f}
+        s = timer.stats()
+        assert (s.frames_timed, s.frames_failed, s.frames_skipped, s.frames_dropped) == (2 * hip.RING_DEPTH + 1, 0, 0, 1)
+    finally:
+        timer.close()
+
+
+def test_tickets_may_come_back_out_of_order_and_are_read_in_submission_order(ctx, small):
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, len(prep.kernels))
+    try:
+        _, a = encode_frame(prep, timer, 1)
+        _, b = encode_frame(prep, timer, 2)
+        assert timer.in_flight() == 2
+        timer.submitted(b)
+        timer.submitted(a)
+        ctx.synchronize()
+        assert [f for f, _ in timer.collect()] == [2, 1]
+    finally:
+        timer.close()
+
+
+def test_an_invalidated_frame_after_a_lap_is_counted_and_never_read(ctx, small):
+    """gpu/timer.rs:1020-1083: the frame lands on a slot whose events hold an
+    earlier lap's times; marked before collection, it is dropped unread, and
+    the frames after it are reported as themselves."""
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, len(prep.kernels))
+    try:
+        for f in range(hip.RING_DEPTH):
+            assert len(run_frame(ctx, prep, timer, f)) == 1
+        marked = hip.RING_DEPTH
+        _, r = encode_frame(prep, timer, marked)
         timer.submitted(r)
         ctx.synchronize()
-        assert [f for f, _ in timer.collect()] == [1]
-        assert timer.stats().frames_dropped == 1
+        assert timer.invalidate_submitted() == 1
+        assert timer.in_flight() == 1
+        assert timer.collect() == []
+        assert timer.in_flight() == 0
+        for f in range(marked + 1, marked + 2 + hip.RING_DEPTH):
+            got = run_frame(ctx, prep, timer, f)
+            assert [x for x, _ in got] == [f] and {t for t, _ in got[0][1]} == {1000 + f}
+        s = timer.stats()
+        assert (s.frames_failed, s.frames_timed, s.frames_skipped) == (1, 2 * hip.RING_DEPTH + 1, 0)
+    finally:
+        timer.close()
+
+
+def test_a_held_frame_is_read_only_once_accepted(ctx, small):
+    """gpu/timer.rs:1086-1160: held frames are read only once accepted and in
+    submission order; the rejected one between two accepted ones is dropped
+    unread and holds back nothing."""
+    _, _, _, prep = small
+    timer = hip.Timer(ctx, len(prep.kernels))
+
+    def held(frame):
+        _, r = encode_frame(prep, timer, frame, tags=[1000 + frame] * len(prep.kernels))
+        h = timer.submitted_held(r)
+        assert h != 0
+        return h
+
+    try:
+        for f in range(hip.RING_DEPTH):
+            h = held(f)
+            ctx.synchronize()
+            assert timer.collect() == []  # completed, not accepted
+            assert timer.verdict(h, True)
+            assert [x for x, _ in timer.collect()] == [f]
+        first = hip.RING_DEPTH
+        before, rejected, after = held(first), held(first + 1), held(first + 2)
+        ctx.synchronize()
+        assert timer.collect() == [] and timer.in_flight() == 3
+        assert timer.verdict(after, True)
+        assert timer.collect() == [] and timer.in_flight() == 3
+        assert timer.verdict(rejected, False)
+        assert timer.verdict(before, True)
+        got = timer.collect()
+        assert [x for x, _ in got] == [first, first + 2]
+        assert {t for t, _ in got[0][1]} == {1000 + first} and {t for t, _ in got[1][1]} == {1000 + first + 2}
+        assert timer.in_flight() == 0
+        assert not timer.verdict(before, False)  # spent
+        s = timer.stats()
+        assert (s.frames_failed, s.frames_timed, s.frames_skipped) == (1, hip.RING_DEPTH + 2, 0)
     finally:
         timer.close()
 
