@@ -128,6 +128,26 @@ __device__ __forceinline__ void split_bf16(float x, __bf16 &hi, __bf16 &lo) {
     hi = (__bf16)x;
     lo = (__bf16)(x - (float)hi);
 }
+// The same split for two values at once: each conversion then rounds a pair
+// (v_cvt_pk_bf16_f32), the same roundings as two split_bf16 calls.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split2_bf16(float a, float b, bf16x2 &hi, bf16x2 &lo) {
+    const f32x2 v = {a, b};
+    hi = __builtin_convertvector(v, bf16x2);
+    lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x2), bf16x2);
+}
+// Eight values (v[0..7]) into hi and lo bf16x8 operands.
+__device__ __forceinline__ void split8_bf16(const float (&v)[8], bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        bf16x2 h, l;
+        split2_bf16(v[e], v[e + 1], h, l);
+        hi[e] = h[0];
+        hi[e + 1] = h[1];
+        lo[e] = l[0];
+        lo[e + 1] = l[1];
+    }
+}
 
 
 // ---- f32 activations kept as hi and lo bf16 planes ----
@@ -154,11 +174,13 @@ __device__ __forceinline__ void store_f32x4(float *base, uint64_t i, f32x4 v, ui
     if (planes) {
         bf16x4 h, l;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            __bf16 hh, ll;
-            split_bf16(v[e], hh, ll);
-            h[e] = hh;
-            l[e] = ll;
+        for (int e = 0; e < 4; e += 2) {
+            bf16x2 hh, ll;
+            split2_bf16(v[e], v[e + 1], hh, ll);
+            h[e] = hh[0];
+            h[e + 1] = hh[1];
+            l[e] = ll[0];
+            l[e + 1] = ll[1];
         }
         *(bf16x4 *)((__bf16 *)base + i) = h;
         *(bf16x4 *)((__bf16 *)base + planes + i) = l;

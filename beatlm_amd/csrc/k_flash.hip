@@ -310,13 +310,10 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
 #pragma unroll
         for (int ds = 0; ds < 4; ds++) {
             if constexpr (SPLIT) {
+                float qv[8];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    __bf16 hi, lo;
-                    split_bf16((e < 4 ? qa[ds][e] : qb[ds][e - 4]) * c, hi, lo);
-                    qh[ds][e] = hi;
-                    ql[ds][e] = lo;
-                }
+                for (int e = 0; e < 8; e++) qv[e] = (e < 4 ? qa[ds][e] : qb[ds][e - 4]) * c;
+                split8_bf16(qv, qh[ds], ql[ds]);
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; e++) qh[ds][e] = (_Float16)((float)q16[ds][e] * c);
@@ -466,15 +463,13 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
                 for (int st2 = 0; st2 < 4; st2++) {
                     const int mb = st2 >> 1, hf = st2 & 1;
                     V8 ph, pl;
+                    float pv[8];
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        const float p = s_cur[mb][8 * hf + e];
-                        __bf16 hi, lo;
-                        split_bf16(p, hi, lo);
-                        ph[e] = hi;
-                        pl[e] = lo;
-                        psum += p;
+                        pv[e] = s_cur[mb][8 * hf + e];
+                        psum += pv[e];
                     }
+                    split8_bf16(pv, ph, pl);
 #pragma unroll
                     for (int db = 0; db < 2; db++) {
                         const int off = db * 32 * ROWB + (((2 * st2 + h) ^ x) << 4);
