@@ -328,6 +328,68 @@ def pmc_kernels(directories: list[str]) -> str:
     return "\n".join(lines) + "\n"
 
 
+def counter_table(directories: list[str]) -> str:
+    """Every counter of rocprofv3 --pmc runs (one directory per pass), mean
+    per dispatch, per kernel and grid size, with the shares the issue and wait
+    counters give: SQ_WAIT_INST_ANY, SQ_WAIT_ANY and SQ_ACTIVE_INST_ANY over
+    SQ_WAVE_CYCLES; SQ_VALU_MFMA_COEXEC_CYCLES over SQ_VALU_MFMA_BUSY_CYCLES."""
+    import re
+
+    per: dict[str, dict[str, list[float]]] = {}
+    for d in directories:
+        for key, name, c, v, t0, t1 in _counter_rows(d):
+            name = re.sub(r"^void ", "", name)
+            name = re.sub(r"bl::\(anonymous namespace\)::", "", name)
+            name = re.sub(r"\(bl::\w+\)$", "", name).replace("(bl::Math)", "M")
+            per.setdefault(name, {}).setdefault(c, []).append(v)
+    lines = []
+    for name, cs in per.items():
+        if not any(k.startswith("SQ_") for k in cs):
+            continue
+        m = {c: sum(v) / len(v) for c, v in cs.items()}
+        lines.append(name)
+        for c in sorted(m):
+            lines.append(f"    {c:32s} {m[c]:16.0f}")
+        wc = m.get("SQ_WAVE_CYCLES")
+        for c in ("SQ_WAIT_INST_ANY", "SQ_WAIT_ANY", "SQ_ACTIVE_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_LDS"):
+            if wc and c in m:
+                lines.append(f"    {c + ' / SQ_WAVE_CYCLES':48s} {m[c] / wc:8.1%}")
+        if m.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in m:
+            lines.append(f"    {'COEXEC / MFMA_BUSY':48s} {m['SQ_VALU_MFMA_COEXEC_CYCLES'] / m['SQ_VALU_MFMA_BUSY_CYCLES']:8.1%}")
+    return "\n".join(lines) + "\n"
+
+
+def attention_only(ctx, cases: list[str], repeats: int) -> list[dict]:
+    """The flash attention spec alone (T, H, f32 or f16 per case, d = 64,
+    uniform qkv in [-1, 1]): per-launch time over `repeats` back-to-back
+    launches and the rate of its 4 T^2 H d flop."""
+    out = []
+    for case in cases:
+        t, h, dt = case.split(",")
+        t, h = int(t), int(h)
+        dtype = hip.F16 if dt == "f16" else hip.F32
+        g = ir.Graph()
+        g.tensor(0, ir.INPUT, t * 3 * h * 64)
+        g.tensor(1, ir.ACTIVATION, t * h * t)
+        g.push(ir.op(ir.OP_ATTENTION_SCORES, [0], [t, h, 64]), 1)
+        g.tensor(2, ir.ACTIVATION, t * h * t)
+        g.push(ir.op(ir.OP_SCALE, [1], [t * h * t], 0.125), 2)
+        g.tensor(3, ir.ACTIVATION, t * h * t)
+        g.push(ir.op(ir.OP_SOFTMAX, [2], [t * h, t]), 3)
+        g.tensor(4, ir.OUTPUT, t * h * 64)
+        g.push(ir.op(ir.OP_ATTENTION_VALUES, [3, 0], [t, h, 64]), 4)
+        prep = ir.prepare(ctx, g, dtype=dtype)
+        rng = np.random.default_rng(1)
+        prep.write(0, rng.uniform(-1, 1, t * 3 * h * 64).astype(np.float16 if dtype == hip.F16 else np.float32))
+        prep.kernels.time(0, repeats)  # clocks up
+        us = prep.kernels.time(0, repeats)
+        fl = 4.0 * t * t * h * 64
+        out.append({"tokens": t, "heads": h, "dtype": dt, "kernel": prep.kernels.label(0), "us_per_launch": round(us, 2),
+                    "TFLOP/s": round(fl / us / 1e6, 1)})
+        prep.close()
+    return out
+
+
 def layernorm_hbm(ctx, rows: int, width: int, repeats: int = 20) -> dict:
     """One LayerNorm of `rows` x `width` f32 rows, larger than the caches, timed
     alone: algorithmic bytes (read x, write y, read gamma and beta) over the
@@ -666,6 +728,10 @@ def main() -> int:
     ap.add_argument("--pmc-kernels", metavar="DIR", nargs="+",
                     help="write the per-kernel counter summary of rocprofv3 --pmc runs and exit")
     ap.add_argument("--trace-summary", metavar="DIR", help="write the kernel statistics of a kernel trace and exit")
+    ap.add_argument("--counter-table", metavar="DIR", nargs="+",
+                    help="write every counter of rocprofv3 --pmc runs per kernel and exit")
+    ap.add_argument("--attention-only", metavar="T,H,DTYPE", nargs="+",
+                    help="time the flash attention spec alone for each case (e.g. 5477,6,f16) and exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run 256 MiB device copies (the traffic counters' calibration) and exit")
     ap.add_argument("--other-configs", default="vit-b-518,vit-l-518x4,vit-s-1036",
@@ -685,6 +751,9 @@ def main() -> int:
     if args.trace_summary:
         sys.stdout.write(trace_summary(args.trace_summary))
         return 0
+    if args.counter_table:
+        sys.stdout.write(counter_table(args.counter_table))
+        return 0
     if args.copy_calibration:
         copy_calibration()
         return 0
@@ -699,6 +768,10 @@ def main() -> int:
     ctx = hip.Context(0)
     if args.f32_math == "mfma":
         ctx.set_f32_math(hip.F32_MATH_MFMA_F32)
+    if args.attention_only:
+        for r in attention_only(ctx, args.attention_only, args.kernel_repeats):
+            print(json.dumps(r), flush=True)
+        return 0
     cfg = CONFIGS[args.config]
     prep, infos, groups, per_launch, mfma_peak, elt, main_line = measure_encoder(
         ctx, args.config, args.steps, args.warmup, args.kernel_repeats, args.f32_math,
@@ -719,6 +792,8 @@ def main() -> int:
         flops = sum(kernel_flops(infos[k]) for k in ks)
         nbytes = sum(kernel_bytes(infos[k], elt) for k in ks)
         hbm = traffic.get((tag, group))
+        if hbm is None:  # the same group measured under another tag
+            hbm = next((v for (_, g), v in traffic.items() if g == group), None)
         common = {"kernel": group, "launches": len(ks), "us_per_launch": round(t / len(ks), 2),
                   "algorithmic_bytes_per_launch": int(nbytes / len(ks)),
                   "traffic": int(hbm) if hbm is not None else None}
@@ -760,6 +835,7 @@ def main() -> int:
         "attention": attn,
         "per_kernel_us": main_line["per_kernel_us"],
         "kernel_sum_us_per_block": main_line["kernel_sum_us_per_block"],
+        "device_memory": main_line["device_memory"],
     }
     if "parity" in main_line:
         result["parity"] = main_line["parity"]
