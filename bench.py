@@ -152,6 +152,40 @@ def kernel_bytes(info, elt: int) -> float:
     return 0.0
 
 
+def step_distribution(ctx, step, n: int) -> dict:
+    """`n` more steps, each between two hipEvents recorded on the backend's
+    stream (no synchronisation between steps): the median, p10 and p90 of
+    the per-step times in µs."""
+    import ctypes as C
+
+    rt = C.CDLL("libamdhip64.so")
+    rt.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    rt.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+    rt.hipEventSynchronize.argtypes = [C.c_void_p]
+    rt.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    rt.hipEventDestroy.argtypes = [C.c_void_p]
+    stream = ctx._lib.bl_ctx_stream(ctx.handle)
+    events = [C.c_void_p() for _ in range(n + 1)]
+    for e in events:
+        assert rt.hipEventCreate(C.byref(e)) == 0
+    ctx.synchronize()
+    assert rt.hipEventRecord(events[0], stream) == 0
+    for i in range(n):
+        step()
+        assert rt.hipEventRecord(events[i + 1], stream) == 0
+    assert rt.hipEventSynchronize(events[n]) == 0
+    us = []
+    for i in range(n):
+        ms = C.c_float()
+        assert rt.hipEventElapsedTime(C.byref(ms), events[i], events[i + 1]) == 0
+        us.append(ms.value * 1e3)
+    for e in events:
+        rt.hipEventDestroy(e)
+    us.sort()
+    pick = lambda q: us[min(n - 1, int(q * n))]
+    return {"n": n, "median": round(pick(0.5), 2), "p10": round(pick(0.1), 2), "p90": round(pick(0.9), 2)}
+
+
 def bracketed(ctx, prep, ks, repeats):
     """Per-launch µs of each kernel in `ks` (alone, back to back), between two
     zero-length spin launches that mark the span in a counter profile."""
@@ -685,6 +719,9 @@ def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_m
 
     ms_per_step = elapsed * 1e3 / steps
     us_per_block = ms_per_step * 1e3 / (cfg["blocks"] * frames)
+    # The spread over single steps (after the timed region, which stays the
+    # K steps between synchronisations).
+    spread = step_distribution(ctx, step, max(steps, 100) if frames == 1 else steps)
     n_kernels = len(prep.kernels)
     per_launch = [prep.kernels.time(k, repeats) for k in range(n_kernels)]
     infos = [prep.program.kernel(k) for k in range(n_kernels)]
@@ -702,6 +739,7 @@ def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_m
         "tokens": tokens, "blocks": cfg["blocks"], "frames": frames, "dtype": cfg["dtype"], "matrix_math": math_name,
         "value": round(us_per_block, 2), "unit": "us/block", "ms_per_step": round(ms_per_step, 4),
         "kernels_per_frame": n_kernels, "device_memory": device_memory,
+        "step_us": spread,
         "per_kernel_us": {g: round(statistics.mean(per_launch[k] for k in ks), 2) for g, ks in groups.items()},
         "kernel_sum_us_per_block": round(sum(per_launch) / cfg["blocks"], 2),
     }
@@ -836,6 +874,7 @@ def main() -> int:
         "per_kernel_us": main_line["per_kernel_us"],
         "kernel_sum_us_per_block": main_line["kernel_sum_us_per_block"],
         "device_memory": main_line["device_memory"],
+        "step_us": main_line["step_us"],
     }
     if "parity" in main_line:
         result["parity"] = main_line["parity"]
