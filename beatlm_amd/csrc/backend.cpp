@@ -352,7 +352,15 @@ struct Launch {
     // A flash kernel whose QKV projections write its K and Vt (fl.prepped):
     // those projection kernels (one per part).
     std::vector<uint32_t> kv_producers;
+    // A LayerNorm folded into the product that reads it (fold >= 0): the
+    // LayerNorm itself launches nothing, the product applies it (FOLD_CONSUMER),
+    // and the product that wrote its input leaves the input's statistics
+    // (FOLD_PRODUCER). Both the LayerNorm and the consumer first make the
+    // statistics from x when the producer has not written them since x changed.
+    int fold = -1;
+    int fold_role = 0;
 };
+enum FoldRole : int { FOLD_NONE = 0, FOLD_LAYER_NORM = 1, FOLD_CONSUMER = 2, FOLD_PRODUCER = 3 };
 
 struct Kernel {
     std::string label;
@@ -372,6 +380,32 @@ struct Pack {
     uint64_t dst_offset;  // into the kernels' pack buffer
     bool stale = true;
     bool dynamic = false;
+    // A folded LayerNorm's pack: B's rows scaled by gamma, then the column
+    // vectors c and d (PackArgs) at vec_offset. Its sources: gamma, beta and
+    // the bias (null when the product has none), each an arena range.
+    struct Source {
+        const void *ptr = nullptr;
+        uint32_t arena = 0;
+        uint64_t offset = 0, size = 0;
+    };
+    Source gamma, beta, bias;
+    uint64_t vec_offset = 0;
+    bool used = false;
+    bool folded() const { return gamma.ptr != nullptr; }
+    bool reads(uint32_t a, uint64_t off, uint64_t bytes) const {
+        auto hit = [&](uint32_t ar, uint64_t o, uint64_t sz) { return sz && ar == a && off < o + sz && o < off + bytes; };
+        return hit(arena, offset, size) || hit(gamma.arena, gamma.offset, gamma.size) ||
+               hit(beta.arena, beta.offset, beta.size) || hit(bias.arena, bias.offset, bias.size);
+    }
+};
+
+// One LayerNorm folded into the product that reads its output. Per binding
+// set: x's bytes (the LayerNorm's input) and the statistics launch that makes
+// the fold's buffers from x.
+struct Fold {
+    uint32_t ln, consumer, producer;
+    std::vector<const char *> x_lo, x_hi;
+    std::vector<LnStatsArgs> stats;
 };
 
 const char *main_name(uint32_t m) {
@@ -539,10 +573,17 @@ struct KvState {
 // A range of kernels captured once as a HIP graph and replayed by
 // bl_kernels_encode_range: one submission instead of one per launch. `kv`
 // is what the attention scratch holds after a replay.
+// Whether each (fold, set)'s statistics describe x as it now is, and which
+// entries a range of launches set (what a graph replay of the range does).
+struct FoldState {
+    std::vector<uint8_t> valid, touched;
+};
+
 struct RangeGraph {
     uint32_t first, count, set;
     hipGraphExec_t exec;
     KvState kv;
+    FoldState folds;  // the entries the range sets (touched) and their values after it
 };
 
 struct bl_kernels {
@@ -558,6 +599,8 @@ struct bl_kernels {
     void *pack_buffer = nullptr;
     uint64_t packs_made = 0;
     KvState kv;
+    std::vector<Fold> folds;
+    FoldState fold_state;  // [fold * sets + set]
     std::vector<RangeGraph> graphs;
     // Graphs replay fixed launches: not used when a kernel of the program
     // rewrites a packed weight's source (the pack must rerun in between),
@@ -567,9 +610,11 @@ struct bl_kernels {
 
 static void kernels_written(bl_kernels *k, uint32_t arena, uint64_t offset, uint64_t bytes) {
     for (Pack &pk : k->packs)
-        if (pk.arena == arena && offset < pk.offset + pk.size && pk.offset < offset + bytes) pk.stale = true;
+        if (pk.reads(arena, offset, bytes)) pk.stale = true;
     // The attention scratch is made from qkv: any host write may have changed it.
     k->kv = KvState{};
+    // So may any folded LayerNorm's input.
+    std::fill(k->fold_state.valid.begin(), k->fold_state.valid.end(), 0);
 }
 
 namespace {
@@ -662,6 +707,184 @@ void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, co
                     if (at != std::string::npos) K.label.replace(at, 9, L.gemm.kslices == 2 ? " 32x64 bk64" : " 32x64");
                 }
             }
+        }
+    }
+}
+
+// Resolves binding `b` of spec `s` through binding set `set`'s substitutions.
+bl_binding resolve(const bl_spec &s, uint32_t b, const bl_binding_set &set) {
+    bl_binding bd = s.bindings[b];
+    for (uint32_t t = 0; t < set.count; t++)
+        if (set.items[t].original == bd.tensor) {
+            bd.arena = set.items[t].arena;
+            bd.offset = set.items[t].offset;
+        }
+    return bd;
+}
+
+// LayerNorms folded into the products that read them. A LayerNorm L (no
+// epilogue, whole) over x [rows][D] whose output n is internal and read by
+// nothing but one later product G, as G's A (G whole, the ring kernel, plain
+// rows, k = D, D a multiple of 32), while x was last written by a product P
+// before L (whole, no split k, its output exactly x, whole 32-column blocks
+// per wave) and nothing writes x between L and G:
+//   LN(x) W + b = rstd (x (gamma W) - mean c) + d,  c = column sums of gamma W,
+//   d = beta W + b,
+// so G reads x itself (its bf16 planes for bf16x3) with a pack of gamma W and
+// applies mean and rstd per row in its epilogue; P's epilogue leaves each
+// row's 32-column block statistics (and the planes). L launches nothing.
+void plan_folds(bl_kernels *ks, const bl_spec *specs, uint32_t n, const bl_binding_set *sets, uint32_t n_sets,
+                const uint32_t *internal, uint32_t n_internal) {
+    if (!n_internal || getenv("BL_NO_LN_FOLD")) return;
+    std::vector<uint32_t> ids(internal, internal + n_internal);
+    std::sort(ids.begin(), ids.end());
+    auto is_internal = [&](uint32_t t) { return std::binary_search(ids.begin(), ids.end(), t); };
+    auto overlaps = [](const Launch &L, const char *lo, const char *hi) { return L.out_lo < hi && lo < L.out_hi; };
+    std::vector<uint8_t> producing(n, 0);
+    for (uint32_t li = 0; li < n; li++) {
+        const bl_spec &ls = specs[li];
+        if (ls.main != BL_MAIN_LAYER_NORM || ls.n_epilogue || ls.part.count != 1) continue;
+        const uint32_t out_t = ls.bindings[ls.n_bindings - 1].tensor;
+        if (!is_internal(out_t)) continue;
+        const uint32_t D = ls.dims[1];
+        if (D % 32 != 0 || ls.part.start != 0 || ls.part.end != ls.dims[0]) continue;
+        // The one reader of the LayerNorm's output: a later product's A.
+        int gi = -1;
+        bool ok = true;
+        for (uint32_t ki = 0; ki < n && ok; ki++) {
+            const bl_spec &s = specs[ki];
+            for (uint32_t b = 0; b + 1 < s.n_bindings; b++) {
+                if (s.bindings[b].tensor != out_t) continue;
+                if (gi >= 0 || ki <= li || s.main != BL_MAIN_MATMUL || b != s.reads[0]) ok = false;
+                else gi = (int)ki;
+            }
+        }
+        if (!ok || gi < 0) continue;
+        const bl_spec &gs = specs[gi];
+        if (gs.part.count != 1) continue;
+        for (uint32_t b = 0; b + 1 < gs.n_bindings; b++)
+            if (b != gs.reads[0] && gs.bindings[b].tensor == out_t) ok = false;
+        int pi = -1;
+        for (uint32_t si = 0; si < n_sets && ok; si++) {
+            const Launch &Ln = ks->kernels[li].per_set[si];
+            const Launch &G = ks->kernels[gi].per_set[si];
+            // The consumer's prologue takes one quad of invocations per tile row
+            // and whole pairs of 32-column blocks, at most 16 of them.
+            if (Ln.family != Family::LAYER_NORM || G.family != Family::GEMM || !G.gemm.pipeline || G.gemm.load != 0 ||
+                4 * gemm_tile_rows(G.tile) > 256 || D > 1024 || D % 64 != 0 ||
+                G.gemm.ksplit > 1 || G.gemm.k != D || G.gemm.m != ls.dims[0] || G.gemm.row0 != 0 || G.gemm.row1 != G.gemm.m) {
+                ok = false;
+                break;
+            }
+            const bl_binding xb = resolve(ls, ls.reads[0], sets[si]);
+            const char *x_lo = (const char *)Ln.ln.x, *x_hi = x_lo + xb.size;
+            // Nothing writes x between the LayerNorm and its reader.
+            for (uint32_t j = li + 1; j < (uint32_t)gi && ok; j++)
+                if (overlaps(ks->kernels[j].per_set[si], x_lo, x_hi)) ok = false;
+            // x's last writer before the LayerNorm, a product writing exactly x.
+            int p = -1;
+            for (uint32_t j = li; j-- > 0;)
+                if (overlaps(ks->kernels[j].per_set[si], x_lo, x_hi)) {
+                    p = (int)j;
+                    break;
+                }
+            if (p < 0 || (pi >= 0 && p != pi) || producing[p]) {
+                ok = false;
+                break;
+            }
+            pi = p;
+            const Launch &P = ks->kernels[p].per_set[si];
+            const bl_spec &ps = specs[p];
+            if (P.family != Family::GEMM || ps.part.count != 1 || P.gemm.ksplit > 1 || P.gemm.flash_ops || P.gemm.c_planes ||
+                P.out_lo != x_lo || P.out_hi != x_hi || P.gemm.n != D || P.gemm.m != ls.dims[0] || P.gemm.row0 != 0 ||
+                P.gemm.row1 != P.gemm.m || (gemm_tile_cols(P.tile) / 2) % 32 != 0 || P.math != G.math)
+                ok = false;
+        }
+        if (!ok || pi < 0) continue;
+        const uint32_t f = (uint32_t)ks->folds.size();
+        Fold fo{li, (uint32_t)gi, (uint32_t)pi, {}, {}, {}};
+        producing[pi] = 1;
+        for (uint32_t si = 0; si < n_sets; si++) {
+            Launch &Ln = ks->kernels[li].per_set[si];
+            Launch &G = ks->kernels[gi].per_set[si];
+            Launch &P = ks->kernels[pi].per_set[si];
+            const bl_binding xb = resolve(ls, ls.reads[0], sets[si]);
+            fo.x_lo.push_back((const char *)Ln.ln.x);
+            fo.x_hi.push_back((const char *)Ln.ln.x + xb.size);
+            LnStatsArgs sa{};
+            sa.x = Ln.ln.x;
+            sa.rows = ls.dims[0];
+            sa.cols = D;
+            fo.stats.push_back(sa);
+            Ln.fold = G.fold = P.fold = (int)f;
+            Ln.fold_role = FOLD_LAYER_NORM;
+            G.fold_role = FOLD_CONSUMER;
+            P.fold_role = FOLD_PRODUCER;
+            // The consumer's own pack: gamma W with the column vectors.
+            Pack pk = ks->packs[G.pack];
+            pk.stale = true;
+            pk.dynamic = false;
+            auto src = [&](const bl_spec &sp, uint32_t b, const void *ptr) {
+                const bl_binding bd = resolve(sp, b, sets[si]);
+                Pack::Source so;
+                so.ptr = ptr;
+                so.arena = bd.arena;
+                so.offset = bd.offset;
+                so.size = bd.size;
+                return so;
+            };
+            pk.gamma = src(ls, ls.reads[1], Ln.ln.gamma);
+            pk.beta = src(ls, ls.reads[2], Ln.ln.beta);
+            pk.bias = G.gemm.bias ? src(gs, gs.reads[2], G.gemm.bias) : Pack::Source{};
+            int found = -1;
+            for (size_t q = 0; q < ks->packs.size(); q++) {
+                const Pack &o = ks->packs[q];
+                if (o.folded() && o.math == pk.math && o.arena == pk.arena && o.offset == pk.offset && o.k == pk.k &&
+                    o.n == pk.n && o.gamma.ptr == pk.gamma.ptr && o.beta.ptr == pk.beta.ptr && o.bias.ptr == pk.bias.ptr)
+                    found = (int)q;
+            }
+            if (found < 0) {
+                ks->packs.push_back(pk);
+                found = (int)ks->packs.size() - 1;
+            }
+            G.pack = found;
+        }
+        ks->folds.push_back(std::move(fo));
+        ks->kernels[li].label += " > folded into " + std::to_string(gi);
+        ks->kernels[gi].label += " < layernorm " + std::to_string(li);
+        ks->kernels[pi].label += " > row statistics";
+    }
+    ks->fold_state.valid.assign(ks->folds.size() * n_sets, 0);
+    ks->fold_state.touched.assign(ks->folds.size() * n_sets, 0);
+}
+
+// Bytes of a fold's buffers for one binding set: the statistics, then (f32
+// storage in bf16x3) x's planes.
+uint64_t fold_stats_bytes(const Fold &f) { return (uint64_t)f.stats[0].rows * (f.stats[0].cols / 32) * 8; }
+uint64_t fold_plane_bytes(const Fold &f, const Launch &G) {
+    return G.math == Math::SPLIT ? (uint64_t)f.stats[0].rows * f.stats[0].cols * 4 : 0;
+}
+
+// Points the folds' launches at their buffers (after the split activations
+// are chosen: the consumer reads x, or x's planes, whatever it read before).
+void apply_folds(bl_kernels *ks) {
+    for (Fold &f : ks->folds) {
+        for (uint32_t si = 0; si < ks->sets; si++) {
+            Launch &G = ks->kernels[f.consumer].per_set[si];
+            Launch &P = ks->kernels[f.producer].per_set[si];
+            const Launch &Ln = ks->kernels[f.ln].per_set[si];
+            const LnStatsArgs &sa = f.stats[si];
+            const Pack &pk = ks->packs[G.pack];
+            P.gemm.ln_out = sa.stats;
+            P.gemm.ln_shadow = sa.shadow;
+            G.gemm.a = sa.shadow ? sa.shadow : sa.x;
+            G.gemm.a_planes = sa.shadow ? (uint64_t)sa.rows * sa.cols : 0;
+            G.gemm.ln_stats = sa.stats;
+            G.gemm.ln_c = (const float *)((char *)ks->pack_buffer + pk.vec_offset);
+            G.gemm.ln_d = G.gemm.ln_c + pk.n_pad;
+            G.gemm.ln_blocks = sa.cols / 32;
+            G.gemm.ln_eps = Ln.ln.eps;
+            G.gemm.bias = nullptr;
         }
     }
 }
@@ -1089,25 +1312,39 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
         }
         ks->kernels.push_back(std::move(k));
     }
+    plan_folds(ks, specs, n, sets, n_sets, internal, n_internal);
     // The backend's own device memory, one allocation beside the plan's
     // arenas: the packed weights, then the split-k GEMMs' partial sums, then
-    // the attention scratch, each 256-byte aligned.
+    // the attention scratch, then the folded LayerNorms' statistics and
+    // planes, each 256-byte aligned.
     auto align256 = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    for (const Kernel &k : ks->kernels)
+        for (const Launch &L : k.per_set)
+            if (L.pack >= 0) ks->packs[L.pack].used = true;
     uint64_t pack_total = 0;
     for (Pack &pk : ks->packs) {
+        if (!pk.used) continue;  // a plain pack every reader of which took a folded one
         pk.dst_offset = pack_total;
         pack_total += align256(packed_bytes(pk.math, pk.k_pad, pk.n_pad));
+        if (pk.folded()) {
+            pk.vec_offset = pack_total;
+            pack_total += align256((uint64_t)2 * pk.n_pad * sizeof(float));
+        }
         // Written by a kernel of this program: packed again before every launch.
         for (uint32_t ki = 0; ki < n && !pk.dynamic; ki++) {
             const bl_binding &o = specs[ki].bindings[specs[ki].n_bindings - 1];
-            if (o.arena == pk.arena && o.offset < pk.offset + pk.size && pk.offset < o.offset + o.size)
-                pk.dynamic = true;
+            if (pk.reads(o.arena, o.offset, o.size)) pk.dynamic = true;
         }
     }
     for (const Pack &pk : ks->packs)
-        if (pk.dynamic) ks->graphs_ok = false;
+        if (pk.used && pk.dynamic) ks->graphs_ok = false;
     const uint64_t partial_at = pack_total, scratch_at = partial_at + align256(partial_bytes);
-    const uint64_t workspace = scratch_at + align256(scratch_bytes);
+    const uint64_t folds_at = scratch_at + align256(scratch_bytes);
+    uint64_t fold_bytes = 0;
+    for (const Fold &f : ks->folds)
+        fold_bytes += ks->sets * (align256(fold_stats_bytes(f)) +
+                                  align256(fold_plane_bytes(f, ks->kernels[f.consumer].per_set[0])));
+    const uint64_t workspace = folds_at + fold_bytes;
     if (workspace) {
         ks->workspace = (char *)bl_device_alloc(ctx, workspace);
         if (!ks->workspace)
@@ -1171,6 +1408,19 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
         }
     }
     if (n_internal && !getenv("BL_NO_SPLIT_ACTIVATIONS")) keep_split_activations(ks, specs, n, internal, n_internal);
+    if (!ks->folds.empty()) {
+        uint64_t at = folds_at;
+        for (Fold &f : ks->folds)
+            for (uint32_t si = 0; si < ks->sets; si++) {
+                LnStatsArgs &sa = f.stats[si];
+                sa.stats = (float *)(ks->workspace + at);
+                at += align256(fold_stats_bytes(f));
+                const uint64_t planes = fold_plane_bytes(f, ks->kernels[f.consumer].per_set[si]);
+                sa.shadow = planes ? ks->workspace + at : nullptr;
+                at += align256(planes);
+            }
+        apply_folds(ks);
+    }
     if (getenv("BL_NO_GRAPH") || profiler_attached()) ks->graphs_ok = false;
     bl_ctx_retain(ctx);
     arenas->users.push_back(ks);
@@ -1194,6 +1444,29 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
 }
 
 extern "C" uint64_t bl_kernels_packs_made(const bl_kernels *k) { return k ? k->packs_made : 0; }
+
+// Test hook: a fold's device buffers copied out (synchronously): what = 0 its
+// statistics for binding set `set`, 1 the column vectors c then d of its pack.
+extern "C" int bl_kernels_fold_read(bl_kernels *k, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes) {
+    if (!k || !dst || fold >= k->folds.size() || set >= k->sets) return BL_ERR_INVALID_ARGUMENT;
+    const Fold &f = k->folds[fold];
+    const Launch &G = k->kernels[f.consumer].per_set[set];
+    const void *src = nullptr;
+    uint64_t have = 0;
+    if (what == 0) {
+        src = f.stats[set].stats;
+        have = fold_stats_bytes(f);
+    } else {
+        const Pack &pk = k->packs[G.pack];
+        src = (const char *)k->pack_buffer + pk.vec_offset;
+        have = (uint64_t)2 * pk.n_pad * sizeof(float);
+    }
+    if (bytes > have) return BL_ERR_INVALID_ARGUMENT;
+    hipSetDevice(k->ctx->device);
+    hipError_t e = hipStreamSynchronize(k->ctx->stream);
+    if (e == hipSuccess) e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? BL_OK : hip_fail(k->ctx, e, "fold read");
+}
 extern "C" uint64_t bl_kernels_workspace_bytes(const bl_kernels *k) { return k ? k->workspace_bytes : 0; }
 
 extern "C" uint32_t bl_kernels_len(const bl_kernels *k) { return k ? (uint32_t)k->kernels.size() : 0; }
@@ -1206,7 +1479,9 @@ extern "C" const char *bl_kernels_label(const bl_kernels *k, uint32_t i) {
 static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
     Pack &pk = k->packs[L.pack];
     if (!pk.dynamic && !pk.stale) return hipSuccess;
-    PackArgs pa{pk.src, (char *)k->pack_buffer + pk.dst_offset, pk.k, pk.n, pk.k_pad, pk.n_pad};
+    PackArgs pa{pk.src, (char *)k->pack_buffer + pk.dst_offset, pk.k, pk.n, pk.k_pad, pk.n_pad,
+                pk.gamma.ptr, pk.beta.ptr, pk.bias.ptr,
+                pk.folded() ? (float *)((char *)k->pack_buffer + pk.vec_offset) : nullptr};
     hipError_t e = launch_pack(pa, pk.math, s);
     if (e == hipSuccess) {
         pk.stale = false;
@@ -1217,7 +1492,7 @@ static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
 
 static hipError_t launch(const Launch &L, hipStream_t s) {
     switch (L.family) {
-    case Family::LAYER_NORM: return launch_layernorm(L.ln, L.f16, s);
+    case Family::LAYER_NORM: return L.fold_role == FOLD_LAYER_NORM ? hipSuccess : launch_layernorm(L.ln, L.f16, s);
     case Family::GEMM: {
         const hipError_t e = launch_gemm(L.gemm, L.math, L.tile, s);
         return e == hipSuccess && L.gemm.ksplit > 1 ? launch_gemm_reduce(L.gemm, L.f16, s) : e;
@@ -1276,6 +1551,38 @@ static Launch with_kv(const Launch &L, uint32_t i, KvState &kv) {
     return run;
 }
 
+// Kernel i of binding set `set` as the attention scratch (kv) and the folded
+// LayerNorms' statistics (fs) require it, and their state after it: a folded
+// LayerNorm, or its consumer, whose statistics do not describe x as it now is
+// first makes them from x; the fold's producer makes them valid; any other
+// write over a fold's x makes them stale.
+static hipError_t run_one(bl_kernels *k, uint32_t i, uint32_t set, hipStream_t s, KvState &kv, FoldState &fs) {
+    const Launch &L = k->kernels[i].per_set[set];
+    const uint32_t sets = k->sets;
+    if (L.fold >= 0 && (L.fold_role == FOLD_LAYER_NORM || L.fold_role == FOLD_CONSUMER)) {
+        const size_t at = (size_t)L.fold * sets + set;
+        if (!fs.valid[at]) {
+            const hipError_t e = launch_ln_stats(k->folds[L.fold].stats[set], L.f16, s);
+            if (e != hipSuccess) return e;
+            fs.valid[at] = 1;
+            fs.touched[at] = 1;
+        }
+        if (L.fold_role == FOLD_LAYER_NORM) return hipSuccess;
+    }
+    const hipError_t e = launch(with_kv(L, i, kv), s);
+    if (e != hipSuccess) return e;
+    for (size_t f = 0; f < k->folds.size(); f++) {
+        const Fold &fo = k->folds[f];
+        for (uint32_t si = 0; si < sets; si++) {
+            if (!(L.out_lo < fo.x_hi[si] && fo.x_lo[si] < L.out_hi)) continue;
+            const size_t at = f * sets + si;
+            fs.valid[at] = (L.fold == (int)f && L.fold_role == FOLD_PRODUCER && si == set) ? 1 : 0;
+            fs.touched[at] = 1;
+        }
+    }
+    return hipSuccess;
+}
+
 extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, bl_timer *timer, uint32_t tag) {
     if (!k) return BL_ERR_INVALID_ARGUMENT;
     if (kernel >= k->kernels.size()) return fail(k->ctx, BL_ERR_NO_SUCH_KERNEL, "there is no kernel %u", kernel);
@@ -1288,7 +1595,7 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
     }
     const Launch &L = k->kernels[kernel].per_set[set];
     hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
-    if (e == hipSuccess) e = launch(with_kv(L, kernel, k->kv), s);
+    if (e == hipSuccess) e = run_one(k, kernel, set, s, k->kv, k->fold_state);
     if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[kernel].label.c_str());
     if (timer && slice >= 0) bl_timer_slice_end(timer, slice, s);
     return BL_OK;
@@ -1298,13 +1605,16 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
 // capture failed (the caller then launches one by one). The attention
 // scratch is taken to hold nothing when a replay starts, so the graph is
 // right whatever ran before it; `kv` is what it holds after a replay.
-static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, KvState &kv) {
+static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, KvState &kv,
+                                     FoldState &fs) {
     hipStream_t s = k->ctx->stream;
     kv = KvState{};
+    // Likewise no fold's statistics are taken as valid when a replay starts.
+    fs.valid.assign(k->fold_state.valid.size(), 0);
+    fs.touched.assign(k->fold_state.valid.size(), 0);
     if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) return nullptr;
     hipError_t e = hipSuccess;
-    for (uint32_t i = first; i < first + count && e == hipSuccess; i++)
-        e = launch(with_kv(k->kernels[i].per_set[set], i, kv), s);
+    for (uint32_t i = first; i < first + count && e == hipSuccess; i++) e = run_one(k, i, set, s, kv, fs);
     hipGraph_t g = nullptr;
     const hipError_t end = hipStreamEndCapture(s, &g);
     hipGraphExec_t exec = nullptr;
@@ -1335,9 +1645,10 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
             if (g.first == first && g.count == count && g.set == set) found = &g;
         if (!found) {
             KvState after;
-            hipGraphExec_t exec = capture_range(k, first, count, set, after);
+            FoldState folds_after;
+            hipGraphExec_t exec = capture_range(k, first, count, set, after, folds_after);
             if (exec) {
-                k->graphs.push_back({first, count, set, exec, after});
+                k->graphs.push_back({first, count, set, exec, after, folds_after});
                 found = &k->graphs.back();
             } else {
                 k->graphs_ok = false;
@@ -1347,13 +1658,15 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
             hipError_t e = hipGraphLaunch(found->exec, s);
             if (e != hipSuccess) return hip_fail(k->ctx, e, "graph launch");
             k->kv = found->kv;
+            for (size_t q = 0; q < found->folds.touched.size(); q++)
+                if (found->folds.touched[q]) k->fold_state.valid[q] = found->folds.valid[q];
             return BL_OK;
         }
     }
     for (uint32_t i = first; i < first + count; i++) {
         const Launch &L = k->kernels[i].per_set[set];
         hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
-        if (e == hipSuccess) e = launch(with_kv(L, i, k->kv), s);
+        if (e == hipSuccess) e = run_one(k, i, set, s, k->kv, k->fold_state);
         if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
     }
     return BL_OK;
@@ -1372,7 +1685,7 @@ extern "C" int bl_kernels_time(bl_kernels *k, uint32_t kernel, uint32_t set, uin
     // kernel's scratch operands); the timed ones then run the kernel alone,
     // back to back, as it runs in its program.
     if (e == hipSuccess && L.pack >= 0) e = refresh_pack(k, L, s);
-    if (e == hipSuccess) e = launch(with_kv(L, kernel, k->kv), s);
+    if (e == hipSuccess) e = run_one(k, kernel, set, s, k->kv, k->fold_state);
     if (e == hipSuccess) e = hipEventRecord(ev[0], s);
     for (uint32_t r = 0; r < repeats && e == hipSuccess; r++) e = launch(L, s);
     if (e == hipSuccess) e = hipEventRecord(ev[1], s);

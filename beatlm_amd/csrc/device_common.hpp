@@ -51,6 +51,25 @@ __device__ __forceinline__ float row_sum(float v) {
     return v;
 }
 
+// v plus v of the lane DPP control CTRL names (row and bank masks full).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// The sum over the 16 lanes of v's DPP row (lanes 16r .. 16r + 15), in every
+// one of them: swaps of neighbours and of pairs inside each quad, then the
+// mirror images inside each half row and each row (gfx9 DPP has no xor mask
+// beyond a quad): after each step the lanes of the next larger group hold
+// equal sums. No LDS round trip, unlike a shuffle.
+__device__ __forceinline__ float row16_sum(float v) {
+    v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v = dpp_add<0x141>(v);  // row_half_mirror
+    return dpp_add<0x140>(v);  // row_mirror
+}
+// The sum over the 4 lanes of v's quad, in each of them.
+__device__ __forceinline__ float quad_sum(float v) { return dpp_add<0x4E>(dpp_add<0xB1>(v)); }
+
 // ---- the attention's value operand layout ----
 // Position of key k inside a row of the transposed values Vt for the 32 x 32
 // flash kernel: bits 2 and 3 of k swapped, so each 16-key group is stored in

@@ -541,7 +541,49 @@ __global__ void spin_kernel(uint64_t ticks) {
     while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(1);
 }
 
+// A folded LayerNorm's statistics of x made from x itself: one invocation
+// per (row, 32-column block), the block's mean and then its sum of squared
+// deviations from it, as the fold's producer computes them in its epilogue;
+// f32 x also goes to the shadow's hi and lo bf16 planes (rows * cols apart).
+template <typename T>
+__global__ __launch_bounds__(256) void ln_stats_kernel(LnStatsArgs a) {
+    const uint32_t nblk = a.cols / 32;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)a.rows * nblk) return;
+    const uint32_t row = (uint32_t)(i / nblk), blk = (uint32_t)(i % nblk);
+    const uint64_t base = (uint64_t)row * a.cols + blk * 32;
+    const T *x = (const T *)a.x + base;
+    float v[32];
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; e++) {
+        v[e] = to_f32(x[e]);
+        sum += v[e];
+    }
+    const float mean = sum * (1.0f / 32.0f);
+    float sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; e++) sq += (v[e] - mean) * (v[e] - mean);
+    *(f32x2 *)(a.stats + 2 * i) = f32x2{mean, sq};
+    if constexpr (sizeof(T) == 4) {
+        if (a.shadow) {
+            const uint64_t planes = (uint64_t)a.rows * a.cols;
+#pragma unroll
+            for (int e = 0; e < 32; e += 4)
+                store_f32x4((float *)a.shadow, base + e, f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]}, planes);
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_ln_stats(const LnStatsArgs &a, bool f16, hipStream_t s) {
+    const uint64_t n = (uint64_t)a.rows * (a.cols / 32);
+    const dim3 grid((uint32_t)((n + 255) / 256));
+    if (f16) hipLaunchKernelGGL(ln_stats_kernel<_Float16>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(ln_stats_kernel<float>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_layernorm(const LayerNormArgs &a, bool f16, hipStream_t s) {
     if (a.row1 <= a.row0) return hipSuccess;

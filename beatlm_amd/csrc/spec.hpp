@@ -69,6 +69,22 @@ struct GemmArgs {
     // bf16x3 math: A, or C, kept as hi and lo bf16 planes this many elements
     // apart (0: f32).
     uint64_t a_planes, c_planes;
+    // A LayerNorm over this product's output folded into the product that
+    // reads the LayerNorm's output (this product is the fold's producer):
+    // ln_out [m][n / 32] of (mean, sum of squared deviations from that mean)
+    // of each row's 32-column blocks of the output as stored; ln_shadow
+    // (bf16x3) the output once more as hi and lo bf16 planes m * n elements
+    // apart, the consumer's A. Null: none.
+    float *ln_out;
+    void *ln_shadow;
+    // A LayerNorm folded into this product (the fold's consumer): A is the
+    // LayerNorm's input x (its bf16 planes for bf16x3); ln_stats holds x's
+    // block statistics as ln_out does; the packed B holds gamma (.) B row by
+    // row, ln_c [n] its column sums and ln_d [n] = beta . B[:, n] + bias[n],
+    // so that LN(x) B + bias = rstd (x (gamma B) - mean c) + d.
+    const float *ln_stats, *ln_c, *ln_d;
+    uint32_t ln_blocks;   // 32-column blocks of x (k / 32)
+    float ln_eps;
 };
 
 hipError_t launch_gemm_reduce(const GemmArgs &a, bool f16, hipStream_t s);
@@ -78,7 +94,25 @@ struct PackArgs {
     const void *src;
     void *dst;
     uint32_t k, n, k_pad, n_pad;
+    // A folded LayerNorm's weights (null: a plain pack): row k of B is packed
+    // scaled by gamma[k], and vec [2][n_pad] receives c[n] (the column sums of
+    // the packed B as the matrix cores read it) and d[n] = beta . B[:, n] +
+    // bias[n] (bias may be null).
+    const void *gamma, *beta, *bias;
+    float *vec;
 };
+
+// A folded LayerNorm's statistics made from x itself (when the fold's
+// producer has not written them since x last changed): x [rows][cols]
+// (cols a multiple of 32) -> stats [rows][cols / 32] of (mean, sum of squared
+// deviations), and (f32 x, shadow non-null) x as hi and lo bf16 planes.
+struct LnStatsArgs {
+    const void *x;
+    float *stats;
+    void *shadow;
+    uint32_t rows, cols;
+};
+hipError_t launch_ln_stats(const LnStatsArgs &a, bool f16, hipStream_t s);
 
 // The tiled products whose operands are gathered (the unfused attention
 // products and the patch embedding), on the vector ALUs.

@@ -213,6 +213,7 @@ _SIGNATURES = {
     "bl_kernels_time": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_float)]),
     "bl_kernels_packs_made": (C.c_uint64, [_VP]),
     "bl_kernels_workspace_bytes": (C.c_uint64, [_VP]),
+    "bl_kernels_fold_read": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, _VP, C.c_uint64]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
     "bl_flash_attention_static": (C.c_int, [_VP, _VP, _VP, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]),
 }
@@ -395,6 +396,18 @@ class Kernels:
 
     def packs_made(self) -> int:
         return int(self.ctx._lib.bl_kernels_packs_made(self.handle))
+
+    def encode_range(self, first: int, count: int, set_index: int = 0) -> None:
+        self.ctx.check(self.ctx._lib.bl_kernels_encode_range(self.handle, first, count, set_index))
+
+    def fold_read(self, fold: int, what: int, floats: int, set_index: int = 0) -> np.ndarray:
+        """A folded LayerNorm's buffers: what = 0 the statistics, 1 the column
+        vectors c then d (diagnostics)."""
+        out = np.zeros(floats, np.float32)
+        self.ctx.check(
+            self.ctx._lib.bl_kernels_fold_read(self.handle, fold, set_index, what, out.ctypes.data_as(C.c_void_p), out.nbytes)
+        )
+        return out
 
     def time(self, kernel: int, repeats: int = 20, set_index: int = 0) -> float:
         """Average µs of one launch over `repeats` back-to-back launches."""

@@ -319,6 +319,18 @@ uint64_t bl_kernels_packs_made(const bl_kernels *kernels);
  * kernels hold no memory of their own; with the arenas' one allocation, a
  * program's device memory is these two allocations. */
 uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
+/* A LayerNorm whose output only a later product reads, as its A, while its
+ * input x was last written by an earlier product, is folded into the reader:
+ * LN(x) W + b = rstd (x (gamma W) - mean c) + d with c the column sums of
+ * gamma W and d = beta W + b, the writer of x leaving each row's 32-column
+ * block statistics (mean, sum of squared deviations) and the LayerNorm
+ * launching nothing. bl_kernels_fold_read copies fold `fold`'s device
+ * buffers out after waiting for the stream: what = 0 the statistics of set
+ * `set` ([rows][cols / 32] pairs of floats), 1 the vectors c then d (padded
+ * to the pack's columns). Folds are numbered in kernel order. A diagnostic
+ * with no counterpart in the reference (whose kernels run one per spec); the
+ * fold itself changes no kernel's bindings or results beyond rounding. */
+int bl_kernels_fold_read(bl_kernels *kernels, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes);
 
 /* ---- flash attention that allocates nothing ----
  * No counterpart in the reference. For callers that cannot allocate device

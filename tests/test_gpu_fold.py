@@ -1,0 +1,175 @@
+"""LayerNorms folded into the products that read them: LN(x) W + b computed
+as rstd (x (gamma W) - mean c) + d inside the product, with x's row
+statistics left by the product that wrote x. The fold must give the
+LayerNorm-then-product result within the f32 bar (against the oracle's
+LayerNorm and matmul), whatever order the host encodes the kernels in:
+the LayerNorm or its reader encoded alone, x rewritten by the host in
+between, ranges replayed as graphs."""
+
+import numpy as np
+import pytest
+
+import oracle
+from beatlm_amd import hip, ir
+
+pytestmark = pytest.mark.gpu
+
+T, D, M = 1370, 384, 1536
+EPS = 1e-6
+# tensor ids of the three-kernel program below
+V, X, WO, BO, LS, G2, B2, W1, B1 = 0, 1, 2, 3, 4, 5, 6, 7, 8
+X1, N2, H, OUT = 12, 13, 14, 15
+
+
+def values(seed=5, d=D, m=M, t=T, f16=False):
+    rng = np.random.default_rng(seed)
+    dt = np.float16 if f16 else np.float32
+    return {
+        V: rng.uniform(-1, 1, t * d).astype(dt),
+        X: rng.uniform(-2, 2, t * d).astype(dt),
+        WO: rng.uniform(-0.05, 0.05, d * d).astype(dt),
+        BO: rng.uniform(-0.1, 0.1, d).astype(dt),
+        LS: rng.uniform(0.1, 1.0, d).astype(dt),
+        G2: (1 + 0.1 * rng.standard_normal(d)).astype(dt),
+        B2: (0.1 * rng.standard_normal(d)).astype(dt),
+        W1: rng.uniform(-0.05, 0.05, d * m).astype(dt),
+        B1: rng.uniform(-0.1, 0.1, m).astype(dt),
+    }
+
+
+def graph(t=T, d=D, m=M):
+    """x1 = x + ls (.) (v Wo + bo) (the fold's producer), n = LN(x1), out =
+    GELU(n W1 + b1) (its consumer); x1 is an output, n internal."""
+    g = ir.Graph()
+    g.tensor(V, ir.INPUT, t * d)
+    g.tensor(X, ir.INPUT, t * d)
+    for tid, n in [(WO, d * d), (BO, d), (LS, d), (G2, d), (B2, d), (W1, d * m), (B1, m)]:
+        g.tensor(tid, ir.WEIGHT, n)
+    g.tensor(10, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_MATMUL, [V, WO, BO], [t, d, d]), 10)
+    g.tensor(11, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_CHANNEL_SCALE, [10, LS], [t, d]), 11)
+    g.tensor(X1, ir.OUTPUT, t * d)
+    g.push(ir.op(ir.OP_ADD, [11, X], [t * d]), X1)
+    g.tensor(N2, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_LAYER_NORM, [X1, G2, B2], [t, d], EPS), N2)
+    g.tensor(H, ir.ACTIVATION, t * m)
+    g.push(ir.op(ir.OP_MATMUL, [N2, W1, B1], [t, d, m]), H)
+    g.tensor(OUT, ir.OUTPUT, t * m)
+    g.push(ir.op(ir.OP_GELU_ERF, [H], [t * m]), OUT)
+    return g
+
+
+def want_out(x1, v, t=T, d=D, m=M):
+    """The oracle's LayerNorm, matmul and GELU-erf over the given x1."""
+    n = oracle.layernorm(x1, v[G2], v[B2], t, d, EPS)
+    return oracle.gelu_erf(oracle.matmul(n, v[W1], v[B1], t, d, m))
+
+
+def assert_close(got, want, what, abs_tol=oracle.TOLERANCE_ABS, rel_tol=oracle.TOLERANCE_REL):
+    bad = oracle.first_mismatch(got, want, abs_tol, rel_tol)
+    err = float(np.max(np.abs(got.astype(np.float64) - want)))
+    print(f"{what}: max abs error {err:.3e}")
+    assert bad is None, f"{what}: element {bad[0]} is {bad[1]}, the oracle says {bad[2]}; max abs error {err:.3e}"
+
+
+@pytest.fixture()
+def prepared(ctx):
+    preps = []
+
+    def make(math=hip.F32_MATH_SPLIT_BF16, dtype=hip.F32):
+        ctx.set_f32_math(math)
+        p = ir.prepare(ctx, graph(), dtype=dtype)
+        preps.append(p)
+        return p
+
+    yield make
+    for p in preps:
+        p.close()
+    ctx.set_f32_math(hip.F32_MATH_SPLIT_BF16)
+
+
+@pytest.mark.parametrize("math", [hip.F32_MATH_SPLIT_BF16, hip.F32_MATH_MFMA_F32])
+def test_a_folded_layernorm_matches_the_layernorm_then_the_product(ctx, prepared, math):
+    prep = prepared(math)
+    labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+    assert "folded into 2" in labels[1] and "row statistics" in labels[0] and "< layernorm 1" in labels[2], labels
+    v = values()
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    ctx.synchronize()
+    x1 = prep.read(X1)
+    assert_close(prep.read(OUT), want_out(x1, v), f"folded LayerNorm, f32 math {math}")
+    # The producer's statistics: per row and 32-column block, the mean and the
+    # sum of squared deviations of x1 as stored.
+    st = prep.kernels.fold_read(0, 0, T * (D // 32) * 2).reshape(T, D // 32, 2).astype(np.float64)
+    blocks = x1.astype(np.float64).reshape(T, D // 32, 32)
+    mean = blocks.mean(2)
+    np.testing.assert_allclose(st[:, :, 0], mean, atol=1e-6)
+    np.testing.assert_allclose(st[:, :, 1], ((blocks - mean[:, :, None]) ** 2).sum(2), rtol=1e-5, atol=1e-5)
+    # The consumer's column vectors: c = column sums of gamma W, d = beta W + b.
+    vec = prep.kernels.fold_read(0, 1, 2 * M).astype(np.float64)
+    w1 = v[W1].astype(np.float64).reshape(D, M)
+    np.testing.assert_allclose(vec[:M], (v[G2][:, None] * w1).sum(0), atol=2e-5)
+    np.testing.assert_allclose(vec[M:], v[B2] @ w1 + v[B1], atol=2e-5)
+
+
+def test_a_folded_layernorm_in_f16_storage_is_within_the_f16_bar(ctx, prepared):
+    prep = prepared(dtype=hip.F16)
+    v = values(f16=True)
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    ctx.synchronize()
+    x1 = prep.read(X1).astype(np.float32)
+    v32 = {k: a.astype(np.float32) for k, a in v.items()}
+    got = prep.read(OUT).astype(np.float32)
+    err = float(np.max(np.abs(got - want_out(x1, v32))))
+    print(f"folded LayerNorm, f16 storage: max abs error {err:.3e}")
+    assert err <= 2e-2
+
+
+def test_the_folded_kernels_encoded_alone_after_the_host_rewrites_x(ctx, prepared):
+    """x rewritten by the host: the producer's statistics are stale, so the
+    LayerNorm (encoded alone) or its reader (encoded alone, or in a replayed
+    range) makes them from x before the product reads them."""
+    prep = prepared()
+    v = values()
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    for step, encode in enumerate([
+        lambda: (prep.kernels.encode(1), prep.kernels.encode(2)),  # the LayerNorm, then its reader
+        lambda: prep.kernels.encode(2),  # the reader alone
+        lambda: prep.kernels.encode_range(1, 2),  # a range from the LayerNorm (graph replay)
+        lambda: prep.kernels.encode_range(1, 2),  # the same range again
+    ]):
+        x1 = oracle.uniform(40 + step, T * D, -3.0, 3.0)
+        prep.write(X1, x1)
+        encode()
+        ctx.synchronize()
+        assert_close(prep.read(OUT), want_out(x1, v), f"after a host write of x, encoding {step}")
+    # The whole program again: the producer's own statistics are used.
+    prep.run()
+    ctx.synchronize()
+    assert_close(prep.read(OUT), want_out(prep.read(X1), v), "the whole program after the host writes")
+
+
+def test_a_layernorm_whose_input_no_product_wrote_is_not_folded(ctx):
+    """x is the program's input: no product leaves its statistics, and the
+    LayerNorm runs as a kernel of its own."""
+    g = ir.Graph()
+    g.tensor(X1, ir.INPUT, T * D)
+    for tid, n in [(G2, D), (B2, D), (W1, D * M), (B1, M)]:
+        g.tensor(tid, ir.WEIGHT, n)
+    g.tensor(N2, ir.ACTIVATION, T * D)
+    g.push(ir.op(ir.OP_LAYER_NORM, [X1, G2, B2], [T, D], EPS), N2)
+    g.tensor(OUT, ir.OUTPUT, T * M)
+    g.push(ir.op(ir.OP_MATMUL, [N2, W1, B1], [T, D, M]), OUT)
+    prep = ir.prepare(ctx, g)
+    try:
+        labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+        assert not any("folded" in s for s in labels), labels
+    finally:
+        prep.close()
