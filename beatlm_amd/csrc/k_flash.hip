@@ -30,9 +30,17 @@
 //     B operand of O^T = V^T P^T for one 16-key step. The running max is only
 //     raised when a tile's max exceeds it by more than 8 (in log2 units), so
 //     most tiles skip the rescale of O; probabilities stay <= 2^8.
+//     The (head, query tile) pairs are dealt to the 8 XCDs round robin (pair
+//     p to XCD p % 8), and each XCD's units to its own workgroups (workgroup
+//     g runs on XCD g % 8), so every query tile is computed and merged inside
+//     one XCD and its L2.
 //     A segment that covers all keys of its query tile writes the output; one
 //     that covers part of them writes (max, sum, unnormalised output) to
-//     scratch, and attn_merge_kernel combines them.
+//     scratch, and attn_merge_kernel combines them, its workgroups dealt to
+//     the XCDs that computed their tiles. (Merging inside the flash kernel,
+//     each run waiting on its XCD's other runs and reading their results
+//     from the XCD's L2, measured slower than this second launch: 27.0
+//     against 21.8 us at 1370 tokens and 6 heads.)
 //  3. flash16_kernel (f32 math, v_mfma_f32_16x16x4_f32): a workgroup owns 64
 //     queries of one head and one range of key tiles (split when there are
 //     too few query tiles to fill the chip); merged by flash16_merge_kernel.
@@ -208,6 +216,105 @@ __host__ __device__ inline uint32_t run_begin(uint32_t v, uint32_t U, uint32_t G
 // The virtual workgroup whose run holds unit u.
 __host__ __device__ inline uint32_t run_of(uint32_t u, uint32_t U, uint32_t G) { return ((u + 1) * G - 1) / U; }
 
+// XCD x's share of the `pairs` (head, query tile) pairs: pairs x, x + 8,
+// x + 16, ... (n of them), as n * kt units (pair after pair, key tiles
+// inner) dealt in equal contiguous runs to the first G of the XCD's wgs / 8
+// workgroups (local index g / 8 of workgroup g). When every pair can have two
+// runs, the runs are counted so that each lies inside one pair: s per pair,
+// the fewest that keep the longest run as short as floor(wgs / 8 / n) runs
+// would. G is 0 when the XCD has no pair.
+struct XcdShare {
+    uint32_t n, U, G;
+};
+__host__ __device__ inline XcdShare xcd_share(uint32_t pairs, uint32_t kt, uint32_t wgs, uint32_t x) {
+    XcdShare sh;
+    const uint32_t gx = wgs / 8;
+    sh.n = pairs > x ? (pairs - x + 7) / 8 : 0;
+    sh.U = sh.n * kt;
+    sh.G = gx;
+    if (sh.n && 2 * sh.n <= gx) {
+        const uint32_t s0 = gx / sh.n, longest = (kt + s0 - 1) / s0, s = (kt + longest - 1) / longest;
+        sh.G = sh.n * s;
+    }
+    if (sh.G > sh.U) sh.G = sh.U;
+    return sh;
+}
+
+// Partial results of workgroup g's segments: slot 0 holds its run's first
+// segment, slot 1 its last (segments between them cover whole query tiles and
+// write the output). Row r of a slot: QROWS rows of 64 floats, (max, sum)
+// pairs beside.
+template <Math M> __device__ __forceinline__ uint64_t partial_row(uint32_t g, uint32_t slot, uint32_t r) {
+    return ((uint64_t)g * 2 + slot) * query_rows<M>() + r;
+}
+
+// Combines rows [r0, r1) of pair `item` (head item / qtiles, query tile
+// item % qtiles) from the partial results of the XCD-local runs vf .. vl that
+// split its key tiles:
+//   O = sum_r 2^(m_r - m) O_r / sum_r 2^(m_r - m) l_r,
+// folded run by run with a running max, MERGE_BATCH runs at a time (every load
+// of a batch issued before the first is used). One invocation per (row, 4
+// columns) at a time out of `nthreads`.
+constexpr uint32_t MERGE_BATCH = 8;
+template <Math M>
+__device__ __forceinline__ void merge_rows(const FlashArgs &a, uint32_t item, uint32_t r0, uint32_t r1, uint32_t tid,
+                                           uint32_t nthreads) {
+    using T = typename FlashTraits<M>::T;
+    constexpr uint32_t QROWS = query_rows<M>();
+    const uint32_t kt = a.t_pad / KT, H = a.heads, pairs = a.qtiles * H;
+    const uint32_t x = item % 8;
+    const XcdShare sh = xcd_share(pairs, kt, a.wgs, x);
+    const uint32_t u0 = (item / 8) * kt;
+    const uint32_t vf = run_of(u0, sh.U, sh.G), vl = run_of(u0 + kt - 1, sh.U, sh.G);
+    const uint32_t head = item / a.qtiles, qt = item % a.qtiles;
+    // The first run holds this tile in its second slot unless the run starts with it.
+    const uint32_t first_slot = run_begin(vf, sh.U, sh.G) < u0 ? 1 : 0;
+    for (uint32_t w = tid; w < (r1 - r0) * (HD / 4); w += nthreads) {
+        const uint32_t r = r0 + w / (HD / 4), d = (w % (HD / 4)) * 4;
+        const uint32_t q = a.row0 + qt * QROWS + r;
+        if (q >= a.row1) continue;
+        float m = -INFINITY, l = 0.0f;
+        f32x4 acc = {0, 0, 0, 0};
+        for (uint32_t v0 = vf; v0 <= vl; v0 += MERGE_BATCH) {
+            f32x2 st[MERGE_BATCH];
+            f32x4 ov[MERGE_BATCH];
+#pragma unroll
+            for (uint32_t b = 0; b < MERGE_BATCH; b++) {
+                const uint32_t v = v0 + b;
+                st[b] = f32x2{-INFINITY, 0.0f};
+                ov[b] = f32x4{0, 0, 0, 0};
+                if (v <= vl) {
+                    const uint64_t row = partial_row<M>(v * 8 + x, v == vf ? first_slot : 0, r);
+                    st[b] = *(const f32x2 *)(a.stats + 2 * row);
+                    ov[b] = *(const f32x4 *)(a.partial + row * HD + d);
+                }
+            }
+            float m_new = m;
+#pragma unroll
+            for (uint32_t b = 0; b < MERGE_BATCH; b++) m_new = fmaxf(m_new, st[b][0]);
+            const float wa = __builtin_amdgcn_exp2f(m - m_new);
+            l *= wa;
+            acc *= wa;
+#pragma unroll
+            for (uint32_t b = 0; b < MERGE_BATCH; b++) {
+                const float wb = __builtin_amdgcn_exp2f(st[b][0] - m_new);  // 0 for a run past vl
+                l += st[b][1] * wb;
+                acc += ov[b] * wb;
+            }
+            m = m_new;
+        }
+        const float inv = 1.0f / l;
+        if constexpr (M == Math::SPLIT) {
+            store_f32x4((float *)a.out, ((uint64_t)q * H + head) * HD + d, acc * inv, a.out_planes);
+        } else {
+            f16x4 w4;
+#pragma unroll
+            for (int e = 0; e < 4; e++) w4[e] = (_Float16)(acc[e] * inv);
+            *(f16x4 *)((T *)a.out + ((uint64_t)q * H + head) * HD + d) = w4;
+        }
+    }
+}
+
 template <Math M>
 __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
     using Tr = FlashTraits<M>;
@@ -232,13 +339,13 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
     const int l32 = lane & 31, h = lane >> 5;
     const uint32_t H = args.heads, tpad = args.t_pad, Tn = args.tokens;
     const uint32_t kt = tpad / KT;
-    const uint32_t U = args.units;
-    const uint32_t G = args.wgs, g = blockIdx.x;
-    // Consecutive workgroups go to different XCDs (round robin over 8); give
-    // the workgroups of one XCD consecutive runs, so they share heads and key
-    // ranges in that XCD's L2.
-    const uint32_t v = (G % 8 == 0) ? (g % 8) * (G / 8) + g / 8 : g;
-    const uint32_t u_begin = run_begin(v, U, G), u_end = run_begin(v + 1, U, G);
+    const uint32_t pairs = args.qtiles * H;
+    // This workgroup's XCD (g % 8: workgroups are dealt to the XCDs round
+    // robin) and its run among that XCD's workgroups.
+    const uint32_t g = blockIdx.x, xg = g % 8, v = g / 8;
+    const XcdShare sh = xcd_share(pairs, kt, args.wgs, xg);
+    const uint32_t u_begin = v < sh.G ? run_begin(v, sh.U, sh.G) : 0;
+    const uint32_t u_end = v < sh.G ? run_begin(v + 1, sh.U, sh.G) : 0;
 
     constexpr int ESZ = 2;
     const uint64_t plane_bytes = (uint64_t)H * tpad * HD * ESZ;
@@ -253,7 +360,7 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
     uint32_t u = u_begin;
     bool first = true;
     while (u < u_end) {
-        const uint32_t item = u / kt;
+        const uint32_t item = xg + 8 * (u / kt);
         const uint32_t k0 = u % kt;
         const uint32_t left = u_end - u;
         const uint32_t k1 = left < kt - k0 ? k0 + left : kt;
@@ -518,7 +625,7 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
                         }
                     }
             } else {
-                const uint64_t row = ((uint64_t)v * 2 + (first ? 0 : 1)) * QROWS + wave * 32 + l32;
+                const uint64_t row = partial_row<M>(g, first ? 0 : 1, wave * 32 + l32);
                 float *part = args.partial + row * HD;
 #pragma unroll
                 for (int db = 0; db < 2; db++)
@@ -538,71 +645,23 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
     }
 }
 
-// Combines the partial results of the query tiles whose key tiles were spread
-// over more than one run: O = sum_r 2^(m_r - m) O_r / sum_r 2^(m_r - m) l_r,
-// folded run by run with a running max. A workgroup takes 16 rows of one
-// (head, query tile); one invocation per (row, 4 columns). The runs are taken
-// MERGE_BATCH at a time, every load of a batch issued before the first is
-// used, so a row pays one memory round trip per batch instead of one per run.
+// Combines the split pairs' partial results: a workgroup takes MERGE_ROWS
+// rows of one pair, one invocation per (row, 4 columns). Workgroup b runs on
+// XCD b % 8 and takes a pair of that XCD's (p % 8 == b % 8), whose partial
+// results its L2 may still hold.
 constexpr uint32_t MERGE_ROWS = 16;
-constexpr uint32_t MERGE_BATCH = 8;
 template <Math M>
 __global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
-    using T = typename FlashTraits<M>::T;
-    constexpr uint32_t QROWS = query_rows<M>();
-    const uint32_t item = blockIdx.x / (QROWS / MERGE_ROWS);
-    const uint32_t r = (blockIdx.x % (QROWS / MERGE_ROWS)) * MERGE_ROWS + threadIdx.x / (HD / 4);
-    const uint32_t d = (threadIdx.x % (HD / 4)) * 4;
-    const uint32_t kt = a.t_pad / KT, H = a.heads;
-    const uint32_t U = a.units, G = a.wgs;
-    const uint32_t u0 = item * kt;
-    const uint32_t vf = run_of(u0, U, G), vl = run_of(u0 + kt - 1, U, G);
-    if (vf == vl) return;  // one run held the whole tile: written by attn_kernel
-    const uint32_t head = item / a.qtiles, qt = item % a.qtiles;
-    const uint32_t q = a.row0 + qt * QROWS + r;
-    if (q >= a.row1) return;
-    // The first run holds this tile in its second slot unless the run starts with it.
-    const uint32_t first_slot = run_begin(vf, U, G) < u0 ? 1 : 0;
-    float m = -INFINITY, l = 0.0f;
-    f32x4 acc = {0, 0, 0, 0};
-    for (uint32_t v0 = vf; v0 <= vl; v0 += MERGE_BATCH) {
-        f32x2 st[MERGE_BATCH];
-        f32x4 ov[MERGE_BATCH];
-#pragma unroll
-        for (uint32_t b = 0; b < MERGE_BATCH; b++) {
-            const uint32_t v = v0 + b;
-            st[b] = f32x2{-INFINITY, 0.0f};
-            ov[b] = f32x4{0, 0, 0, 0};
-            if (v <= vl) {
-                const uint64_t row = ((uint64_t)v * 2 + (v == vf ? first_slot : 0)) * QROWS + r;
-                st[b] = *(const f32x2 *)(a.stats + 2 * row);
-                ov[b] = *(const f32x4 *)(a.partial + row * HD + d);
-            }
-        }
-        float m_new = m;
-#pragma unroll
-        for (uint32_t b = 0; b < MERGE_BATCH; b++) m_new = fmaxf(m_new, st[b][0]);
-        const float wa = __builtin_amdgcn_exp2f(m - m_new);
-        l *= wa;
-        acc *= wa;
-#pragma unroll
-        for (uint32_t b = 0; b < MERGE_BATCH; b++) {
-            const float wb = __builtin_amdgcn_exp2f(st[b][0] - m_new);  // 0 for a run past vl
-            l += st[b][1] * wb;
-            acc += ov[b] * wb;
-        }
-        m = m_new;
-    }
-    const float inv = 1.0f / l;
-    T *out = (T *)a.out + ((uint64_t)q * H + head) * HD + d;
-    if constexpr (M == Math::SPLIT) {
-        store_f32x4((float *)a.out, ((uint64_t)q * H + head) * HD + d, acc * inv, a.out_planes);
-    } else {
-        f16x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; e++) w[e] = (_Float16)(acc[e] * inv);
-        *(f16x4 *)out = w;
-    }
+    constexpr uint32_t GROUPS = query_rows<M>() / MERGE_ROWS;
+    const uint32_t x = blockIdx.x % 8, k = blockIdx.x / 8;
+    const uint32_t item = x + 8 * (k / GROUPS);
+    const uint32_t r0 = (k % GROUPS) * MERGE_ROWS;
+    if (item >= a.qtiles * a.heads) return;
+    const uint32_t kt = a.t_pad / KT;
+    const XcdShare sh = xcd_share(a.qtiles * a.heads, kt, a.wgs, x);
+    const uint32_t u0 = (item / 8) * kt;
+    if (run_of(u0, sh.U, sh.G) == run_of(u0 + kt - 1, sh.U, sh.G)) return;  // written by attn_kernel
+    merge_rows<M>(a, item, r0, r0 + MERGE_ROWS, threadIdx.x, 256);
 }
 
 // ---- 3. the 16 x 16 kernel (f32 math) ----
@@ -795,7 +854,7 @@ hipError_t launch_32(const FlashArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(attn_kernel<M>, dim3(a.wgs), dim3(THREADS32), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess || !a.merge) return e;
-    const uint32_t blocks = a.qtiles * a.heads * (query_rows<M>() / MERGE_ROWS);
+    const uint32_t blocks = 8 * ((a.qtiles * a.heads + 7) / 8) * (query_rows<M>() / MERGE_ROWS);
     hipLaunchKernelGGL(attn_merge_kernel<M>, dim3(blocks), dim3(MERGE_ROWS * (HD / 4)), 0, s, a);
     return hipGetLastError();
 }
@@ -841,30 +900,16 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
         const uint32_t qrows = m == Math::F16 ? query_rows<Math::F16>() : query_rows<Math::SPLIT>();
         p.qtiles = (rows + qrows - 1) / qrows;
         p.units = (uint64_t)heads * p.qtiles * kt;
-        // One workgroup per CU (its 8 waves are two per SIMD).
-        const uint64_t slots = std::max<uint32_t>(compute_units, 1);
-        p.wgs = (uint32_t)std::min<uint64_t>(p.units, slots);
-        // Few units per CU (T in the low thousands): a run that crosses from
-        // one (head, query tile) to the next pays a second prologue and sets
-        // the kernel's tail. With a multiple of the pairs as the grid every
-        // run lies inside one pair: S runs per pair, the fewest that keep
-        // the longest run as short as floor(CUs / pairs) runs would.
-        const uint64_t pairs = (uint64_t)heads * p.qtiles;
-        if (pairs && pairs * 2 <= slots) {
-            const uint32_t s0 = (uint32_t)(slots / pairs);
-            const uint32_t longest = (kt + s0 - 1) / s0;
-            const uint32_t s = (kt + longest - 1) / longest;
-            p.wgs = (uint32_t)(pairs * s);
+        // One workgroup per CU, the same number on each XCD (its 8 waves are
+        // two per SIMD); the pairs and their units are shared out per XCD.
+        p.wgs = std::max<uint32_t>(8, compute_units / 8 * 8);
+        const uint32_t pairs = heads * p.qtiles;
+        for (uint32_t item = 0; item < pairs && !p.merge; item++) {
+            const XcdShare sh = xcd_share(pairs, kt, p.wgs, item % 8);
+            const uint32_t u0 = (item / 8) * kt;
+            p.merge = run_of(u0, sh.U, sh.G) != run_of(u0 + kt - 1, sh.U, sh.G);
         }
-        if (const char *force = getenv("BL_FLASH_RUNS")) {
-            const long w = atol(force);
-            if (w > 0) p.wgs = (uint32_t)std::min<uint64_t>(p.units, (uint64_t)w);
-        }
-        // The run arithmetic is 32-bit.
-        if (p.units * p.wgs >= (1ull << 32)) p.wgs = (uint32_t)(((1ull << 32) - 1) / p.units);
-        for (uint32_t item = 0; item < heads * p.qtiles && !p.merge; item++)
-            p.merge = run_of(item * kt, (uint32_t)p.units, p.wgs) != run_of(item * kt + kt - 1, (uint32_t)p.units, p.wgs);
-        // Two result slots per run: its first and its last segment.
+        // Two result slots per workgroup: its first and its last segment.
         extra = (uint64_t)p.wgs * 2 * qrows * (HD + 2) * sizeof(float);
     }
     p.scratch_bytes = operand_bytes(m, heads, t_pad) + extra;
