@@ -1177,6 +1177,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 if (const char *force = getenv("BL_GEMM_KGROUPS")) ga.kgroups = (uint32_t)atoi(force);
                 if (const char *force = getenv("BL_GEMM_STAGES")) ga.stages = (uint32_t)atoi(force);
                 ga.kslices = kslices;
+                ga.lane_epilogue = getenv("BL_GEMM_LANE_EPILOGUE") ? 1 : 0;
                 if (const char *force = getenv("BL_GEMM_KSLICES")) ga.kslices = (uint32_t)atoi(force);
                 // A 3x3 convolution with fewer tiles than CUs (the decoder's deep,
                 // narrow stages: 6 tiles and 108 k-steps at 19 x 19 x 384 -> 64)

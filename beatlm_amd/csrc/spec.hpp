@@ -85,6 +85,8 @@ struct GemmArgs {
     const float *ln_stats, *ln_c, *ln_d;
     uint32_t ln_blocks;   // 32-column blocks of x (k / 32)
     float ln_eps;
+    // The ring kernel's per-lane epilogue in place of the one through LDS.
+    uint32_t lane_epilogue;
 };
 
 hipError_t launch_gemm_reduce(const GemmArgs &a, bool f16, hipStream_t s);
