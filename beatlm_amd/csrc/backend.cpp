@@ -584,6 +584,7 @@ struct RangeGraph {
     hipGraphExec_t exec;
     KvState kv;
     FoldState folds;  // the entries the range sets (touched) and their values after it
+    uint32_t launches;  // kernel nodes of the captured graph
 };
 
 struct bl_kernels {
@@ -702,6 +703,7 @@ void keep_split_activations(bl_kernels *ks, const bl_spec *specs, uint32_t n, co
                     L.tile = TILE_32x64;
                     L.gemm.kgroups = 1;
                     L.gemm.stages = 3;
+                    if (const char *force = getenv("BL_GEMM_STAGES")) L.gemm.stages = (uint32_t)atoi(force);
                     L.gemm.kslices = L.gemm.k % 64 == 0 ? 2 : 1;
                     const size_t at = K.label.find(" 64x64 k4");
                     if (at != std::string::npos) K.label.replace(at, 9, L.gemm.kslices == 2 ? " 32x64 bk64" : " 32x64");
@@ -1607,7 +1609,8 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
 // scratch is taken to hold nothing when a replay starts, so the graph is
 // right whatever ran before it; `kv` is what it holds after a replay.
 static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, KvState &kv,
-                                     FoldState &fs) {
+                                     FoldState &fs, uint32_t &launches) {
+    launches = 0;
     hipStream_t s = k->ctx->stream;
     kv = KvState{};
     // Likewise no fold's statistics are taken as valid when a replay starts.
@@ -1621,6 +1624,15 @@ static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t coun
     hipGraphExec_t exec = nullptr;
     if (e == hipSuccess && end == hipSuccess && g) {
         if (hipGraphInstantiate(&exec, g, nullptr, nullptr, 0) != hipSuccess) exec = nullptr;
+        size_t nodes = 0;
+        if (exec && hipGraphGetNodes(g, nullptr, &nodes) == hipSuccess && nodes) {
+            std::vector<hipGraphNode_t> list(nodes);
+            if (hipGraphGetNodes(g, list.data(), &nodes) == hipSuccess)
+                for (size_t q = 0; q < nodes; q++) {
+                    hipGraphNodeType type;
+                    if (hipGraphNodeGetType(list[q], &type) == hipSuccess && type == hipGraphNodeTypeKernel) launches++;
+                }
+        }
     }
     if (g) hipGraphDestroy(g);
     (void)hipGetLastError();
@@ -1647,9 +1659,10 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
         if (!found) {
             KvState after;
             FoldState folds_after;
-            hipGraphExec_t exec = capture_range(k, first, count, set, after, folds_after);
+            uint32_t launches = 0;
+            hipGraphExec_t exec = capture_range(k, first, count, set, after, folds_after, launches);
             if (exec) {
-                k->graphs.push_back({first, count, set, exec, after, folds_after});
+                k->graphs.push_back({first, count, set, exec, after, folds_after, launches});
                 found = &k->graphs.back();
             } else {
                 k->graphs_ok = false;
@@ -1671,6 +1684,17 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
         if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
     }
     return BL_OK;
+}
+
+extern "C" int bl_kernels_range_launches(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, uint32_t *launches) {
+    if (!k || !launches) return BL_ERR_INVALID_ARGUMENT;
+    for (const RangeGraph &g : k->graphs)
+        if (g.first == first && g.count == count && g.set == set) {
+            *launches = g.launches;
+            return BL_OK;
+        }
+    return fail(k->ctx, BL_ERR_INVALID_ARGUMENT, "kernels %u..%u of set %u have no captured graph", first,
+                first + count - 1, set);
 }
 
 extern "C" int bl_kernels_time(bl_kernels *k, uint32_t kernel, uint32_t set, uint32_t repeats, float *micros) {

@@ -30,10 +30,11 @@
 //     B operand of O^T = V^T P^T for one 16-key step. The running max is only
 //     raised when a tile's max exceeds it by more than 8 (in log2 units), so
 //     most tiles skip the rescale of O; probabilities stay <= 2^8.
-//     The (head, query tile) pairs are dealt to the 8 XCDs round robin (pair
-//     p to XCD p % 8), and each XCD's units to its own workgroups (workgroup
-//     g runs on XCD g % 8), so every query tile is computed and merged inside
-//     one XCD and its L2.
+//     The (head, query tile) pairs are dealt to the 8 XCDs in 8 contiguous
+//     blocks, so an XCD's pairs share one or two heads and its L2 fetches
+//     their keys and values once, and each XCD's units to its own workgroups
+//     (workgroup g runs on XCD g % 8), so every query tile is computed and
+//     merged inside one XCD and its L2.
 //     A segment that covers all keys of its query tile writes the output; one
 //     that covers part of them writes (max, sum, unnormalised output) to
 //     scratch, and attn_merge_kernel combines them, its workgroups dealt to
@@ -216,8 +217,9 @@ __host__ __device__ inline uint32_t run_begin(uint32_t v, uint32_t U, uint32_t G
 // The virtual workgroup whose run holds unit u.
 __host__ __device__ inline uint32_t run_of(uint32_t u, uint32_t U, uint32_t G) { return ((u + 1) * G - 1) / U; }
 
-// XCD x's share of the `pairs` (head, query tile) pairs: pairs x, x + 8,
-// x + 16, ... (n of them), as n * kt units (pair after pair, key tiles
+// XCD x's share of the `pairs` (head, query tile) pairs: the n pairs from
+// run_begin(x, pairs, 8) on (the 8 XCDs' contiguous blocks; run_of(p, pairs,
+// 8) is pair p's XCD), as n * kt units (pair after pair, key tiles
 // inner) dealt in equal contiguous runs to the first G of the XCD's wgs / 8
 // workgroups (local index g / 8 of workgroup g). When every pair can have two
 // runs, the runs are counted so that each lies inside one pair: s per pair,
@@ -229,7 +231,7 @@ struct XcdShare {
 __host__ __device__ inline XcdShare xcd_share(uint32_t pairs, uint32_t kt, uint32_t wgs, uint32_t x) {
     XcdShare sh;
     const uint32_t gx = wgs / 8;
-    sh.n = pairs > x ? (pairs - x + 7) / 8 : 0;
+    sh.n = run_begin(x + 1, pairs, 8) - run_begin(x, pairs, 8);
     sh.U = sh.n * kt;
     sh.G = gx;
     if (sh.n && 2 * sh.n <= gx) {
@@ -262,9 +264,9 @@ __device__ __forceinline__ void merge_rows(const FlashArgs &a, uint32_t item, ui
     using T = typename FlashTraits<M>::T;
     constexpr uint32_t QROWS = query_rows<M>();
     const uint32_t kt = a.t_pad / KT, H = a.heads, pairs = a.qtiles * H;
-    const uint32_t x = item % 8;
+    const uint32_t x = run_of(item, pairs, 8);
     const XcdShare sh = xcd_share(pairs, kt, a.wgs, x);
-    const uint32_t u0 = (item / 8) * kt;
+    const uint32_t u0 = (item - run_begin(x, pairs, 8)) * kt;
     const uint32_t vf = run_of(u0, sh.U, sh.G), vl = run_of(u0 + kt - 1, sh.U, sh.G);
     const uint32_t head = item / a.qtiles, qt = item % a.qtiles;
     // The first run holds this tile in its second slot unless the run starts with it.
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
     uint32_t u = u_begin;
     bool first = true;
     while (u < u_end) {
-        const uint32_t item = xg + 8 * (u / kt);
+        const uint32_t item = run_begin(xg, pairs, 8) + u / kt;
         const uint32_t k0 = u % kt;
         const uint32_t left = u_end - u;
         const uint32_t k1 = left < kt - k0 ? k0 + left : kt;
@@ -647,19 +649,20 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
 
 // Combines the split pairs' partial results: a workgroup takes MERGE_ROWS
 // rows of one pair, one invocation per (row, 4 columns). Workgroup b runs on
-// XCD b % 8 and takes a pair of that XCD's (p % 8 == b % 8), whose partial
-// results its L2 may still hold.
+// XCD b % 8 and takes a pair of that XCD's block, whose partial results its
+// L2 may still hold.
 constexpr uint32_t MERGE_ROWS = 16;
 template <Math M>
 __global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
     constexpr uint32_t GROUPS = query_rows<M>() / MERGE_ROWS;
     const uint32_t x = blockIdx.x % 8, k = blockIdx.x / 8;
-    const uint32_t item = x + 8 * (k / GROUPS);
-    const uint32_t r0 = (k % GROUPS) * MERGE_ROWS;
-    if (item >= a.qtiles * a.heads) return;
+    const uint32_t pairs = a.qtiles * a.heads;
+    const uint32_t local = k / GROUPS, r0 = (k % GROUPS) * MERGE_ROWS;
+    if (local >= run_begin(x + 1, pairs, 8) - run_begin(x, pairs, 8)) return;
+    const uint32_t item = run_begin(x, pairs, 8) + local;
     const uint32_t kt = a.t_pad / KT;
-    const XcdShare sh = xcd_share(a.qtiles * a.heads, kt, a.wgs, x);
-    const uint32_t u0 = (item / 8) * kt;
+    const XcdShare sh = xcd_share(pairs, kt, a.wgs, x);
+    const uint32_t u0 = local * kt;
     if (run_of(u0, sh.U, sh.G) == run_of(u0 + kt - 1, sh.U, sh.G)) return;  // written by attn_kernel
     merge_rows<M>(a, item, r0, r0 + MERGE_ROWS, threadIdx.x, 256);
 }
@@ -905,8 +908,9 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
         p.wgs = std::max<uint32_t>(8, compute_units / 8 * 8);
         const uint32_t pairs = heads * p.qtiles;
         for (uint32_t item = 0; item < pairs && !p.merge; item++) {
-            const XcdShare sh = xcd_share(pairs, kt, p.wgs, item % 8);
-            const uint32_t u0 = (item / 8) * kt;
+            const uint32_t x = run_of(item, pairs, 8);
+            const XcdShare sh = xcd_share(pairs, kt, p.wgs, x);
+            const uint32_t u0 = (item - run_begin(x, pairs, 8)) * kt;
             p.merge = run_of(u0, sh.U, sh.G) != run_of(u0 + kt - 1, sh.U, sh.G);
         }
         // Two result slots per workgroup: its first and its last segment.

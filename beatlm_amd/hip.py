@@ -214,6 +214,7 @@ _SIGNATURES = {
     "bl_kernels_packs_made": (C.c_uint64, [_VP]),
     "bl_kernels_workspace_bytes": (C.c_uint64, [_VP]),
     "bl_kernels_fold_read": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, _VP, C.c_uint64]),
+    "bl_kernels_range_launches": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint32)]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
     "bl_flash_attention_static": (C.c_int, [_VP, _VP, _VP, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]),
 }
@@ -389,6 +390,13 @@ class Kernels:
 
     def encode_all(self, set_index: int = 0) -> None:
         self.ctx.check(self.ctx._lib.bl_kernels_encode_range(self.handle, 0, len(self), set_index))
+
+    def range_launches(self, first: int, count: int, set_index: int = 0) -> int:
+        """GPU kernel launches of the captured graph that encode_range(first,
+        count, set_index) replays (raises when that range has no graph)."""
+        n = C.c_uint32()
+        self.ctx.check(self.ctx._lib.bl_kernels_range_launches(self.handle, first, count, set_index, C.byref(n)))
+        return int(n.value)
 
     def workspace_bytes(self) -> int:
         """Device bytes the kernels hold beside the arenas (one allocation)."""

@@ -352,10 +352,16 @@ def pmc_kernels(directories: list[str]) -> str:
         ns = list(k["ns"].values())
         us = sum(ns) / len(ns) / 1e3
         cs = {c: sum(v) / len(v) for c, v in k["counters"].items()}
-        flops = cs.get("MfmaFlopsBF16", 0.0) + cs.get("MfmaFlopsF16", 0.0)
+        # The derived metrics, or the same from the raw counters (MOPS x 512
+        # flop; busy cycles over the GPU-active cycles of one XCD, which
+        # GRBM_GUI_ACTIVE sums over the 8, times the 1024 SIMDs).
+        flops = cs.get("MfmaFlopsBF16", 512.0 * cs.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)) + \
+            cs.get("MfmaFlopsF16", 512.0 * cs.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0))
         tf = flops / us / 1e6
         ta = cs["TA_BUSY_avr"] / (cs["GRBM_GUI_ACTIVE"] / 8) if "TA_BUSY_avr" in cs and cs.get("GRBM_GUI_ACTIVE") else None
         util = cs.get("MfmaUtil")
+        if util is None and "SQ_VALU_MFMA_BUSY_CYCLES" in cs and cs.get("GRBM_GUI_ACTIVE"):
+            util = 100.0 * cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (cs["GRBM_GUI_ACTIVE"] / 8 * 1024)
         lines.append(f"{name[:64]:64s} {len(ns):5d} {us:8.2f} " + (f"{util:9.2f} " if util is not None else f"{'':9s} ") +
                      (f"{tf:12.1f} {tf / PEAK_TFLOPS['bf16']:7.1%} " if flops else f"{'':12s} {'':7s} ") +
                      (f"{ta:7.1%}" if ta is not None else ""))
@@ -723,6 +729,12 @@ def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_m
     # K steps between synchronisations).
     spread = step_distribution(ctx, step, max(steps, 100) if frames == 1 else steps)
     n_kernels = len(prep.kernels)
+    # GPU launches per frame: the kernel nodes of the graph a frame replays
+    # (none when graphs are off, e.g. under a profiler).
+    try:
+        launches = prep.kernels.range_launches(0, n_kernels, 0)
+    except Exception:
+        launches = None
     per_launch = [prep.kernels.time(k, repeats) for k in range(n_kernels)]
     infos = [prep.program.kernel(k) for k in range(n_kernels)]
     groups: dict[str, list[int]] = {}
@@ -738,7 +750,7 @@ def measure_encoder(ctx, name: str, steps: int, warmup: int, repeats: int, f32_m
                     f"(one job slot each), {cfg['dtype']}",
         "tokens": tokens, "blocks": cfg["blocks"], "frames": frames, "dtype": cfg["dtype"], "matrix_math": math_name,
         "value": round(us_per_block, 2), "unit": "us/block", "ms_per_step": round(ms_per_step, 4),
-        "kernels_per_frame": n_kernels, "device_memory": device_memory,
+        "kernels_per_frame": launches, "ir_kernels_per_frame": n_kernels, "device_memory": device_memory,
         "step_us": spread,
         "per_kernel_us": {g: round(statistics.mean(per_launch[k] for k in ks), 2) for g, ks in groups.items()},
         "kernel_sum_us_per_block": round(sum(per_launch) / cfg["blocks"], 2),
@@ -868,6 +880,7 @@ def main() -> int:
             "frames": main_line["frames"],
             "matrix_math": main_line["matrix_math"],
             "kernels_per_frame": main_line["kernels_per_frame"],
+            "ir_kernels_per_frame": main_line["ir_kernels_per_frame"],
         },
         "roofline": roofline,
         "attention": attn,

@@ -331,6 +331,13 @@ uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
  * with no counterpart in the reference (whose kernels run one per spec); the
  * fold itself changes no kernel's bindings or results beyond rounding. */
 int bl_kernels_fold_read(bl_kernels *kernels, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes);
+/* The GPU kernel launches behind one bl_kernels_encode_range(first, count,
+ * set) call, counted as the kernel nodes of the HIP graph that call replays
+ * (a folded LayerNorm adds none; a flash attention adds its merge launch when
+ * it has one). BL_ERR_INVALID_ARGUMENT when that range has no captured graph
+ * (graphs off, or the range not yet encoded). A measurement aid with no
+ * counterpart in the reference. */
+int bl_kernels_range_launches(bl_kernels *kernels, uint32_t first, uint32_t count, uint32_t set, uint32_t *launches);
 
 /* ---- flash attention that allocates nothing ----
  * No counterpart in the reference. For callers that cannot allocate device

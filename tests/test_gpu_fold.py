@@ -154,6 +154,11 @@ def test_the_folded_kernels_encoded_alone_after_the_host_rewrites_x(ctx, prepare
     prep.run()
     ctx.synchronize()
     assert_close(prep.read(OUT), want_out(prep.read(X1), v), "the whole program after the host writes")
+    # GPU launches of the replayed graphs: the folded LayerNorm launches
+    # nothing; from the LayerNorm on, its statistics kernel takes the place of
+    # the producer's.
+    assert prep.kernels.range_launches(0, 3) == 2
+    assert prep.kernels.range_launches(1, 2) == 2
 
 
 def test_a_layernorm_whose_input_no_product_wrote_is_not_folded(ctx):
