@@ -223,7 +223,8 @@ def pmc_summary(directory: str) -> str:
     """The counter summary of a profile directory holding four rocprofv3 --pmc
     runs (pmc_FETCH_SIZE, pmc_WRITE_SIZE of this bench; copy_FETCH_SIZE,
     copy_WRITE_SIZE of a 256 MiB device copy) and the bench's JSON line in
-    pmc_FETCH_SIZE.log. Each counter is scaled by what it reads for the copy
+    pmc_FETCH_SIZE.log (and pmc_WRITE_SIZE.log, when present, for that
+    pass's brackets). Each counter is scaled by what it reads for the copy
     (bytes moved / counter KiB). The dispatches between the bench's marker
     launches (spin_kernel) are the bracketed group's: (repeats + 1) launches of
     each of its kernels."""
@@ -239,13 +240,21 @@ def pmc_summary(directory: str) -> str:
         vals = [float(r["Counter_Value"]) for r in rows(f"copy_{c}") if "copyBuffer" in r["Kernel_Name"]]
         vals.sort()
         scale[c] = copy_bytes / (vals[len(vals) // 2] * 1024.0)
-    with open(os.path.join(directory, "pmc_FETCH_SIZE.log")) as f:
-        line = next(l for l in f if l.startswith("{") and '"metric"' in l)
-    bench = json.loads(line)
+    def brackets(c):
+        # Each pass's own bench line: the groups it bracketed (the dominant
+        # group is chosen per run) in the order of its marker launches.
+        name = f"pmc_{c}.log"
+        if c == "WRITE_SIZE" and not os.path.exists(os.path.join(directory, name)):
+            name = "pmc_FETCH_SIZE.log"
+        with open(os.path.join(directory, name)) as f:
+            line = next(l for l in f if l.startswith("{") and '"metric"' in l)
+        return json.loads(line)["brackets"]
+
     out = [f"# counter scale from a {copy_bytes >> 20} MiB copy: FETCH_SIZE x{scale['FETCH_SIZE']:.4f}, "
            f"WRITE_SIZE x{scale['WRITE_SIZE']:.4f} (bytes per counter KiB / 1024)"]
     per = {}
     for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        bench = {"brackets": brackets(c)}
         rs = rows(f"pmc_{c}")
         marks = [i for i, r in enumerate(rs) if "spin_kernel" in r["Kernel_Name"]]
         spans = [rs[marks[2 * j] + 1: marks[2 * j + 1]] for j in range(len(marks) // 2)]
@@ -260,6 +269,8 @@ def pmc_summary(directory: str) -> str:
                 out.append(f"# {b['tag']:10s} {c:10s} {name:48s} dispatches {len(v):4d}  "
                            f"mean {sum(v) / len(v):12.1f} KiB")
     for (tag, group), cs in per.items():
+        if len(cs) < 2:
+            continue  # bracketed in one pass only
         b = cs["FETCH_SIZE"][2]
         launches = (b["repeats"] + 1) * b["kernels"]
         fetch = cs["FETCH_SIZE"][0] * 1024 * scale["FETCH_SIZE"] / launches
@@ -774,6 +785,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip comparing the timed output with the oracle")
     ap.add_argument("--kernel-repeats", type=int, default=20)
+    ap.add_argument("--roofline-group", default=None,
+                    help="bracket this kernel group as the roofline one (counter profiles, whose timings differ)")
     ap.add_argument("--pmc-summary", metavar="DIR", help="write the counter summary of a profile directory and exit")
     ap.add_argument("--pmc-kernels", metavar="DIR", nargs="+",
                     help="write the per-kernel counter summary of rocprofv3 --pmc runs and exit")
@@ -827,7 +840,7 @@ def main() -> int:
         ctx, args.config, args.steps, args.warmup, args.kernel_repeats, args.f32_math,
         check=not args.no_check and args.config != "vit-l-518x4")
     totals = {g: sum(per_launch[k] for k in ks) for g, ks in groups.items()}
-    dominant = max(totals, key=totals.get)
+    dominant = args.roofline_group if args.roofline_group in totals else max(totals, key=totals.get)
     traffic = read_traffic(args.config, main_line["matrix_math"])
     brackets = []
 
