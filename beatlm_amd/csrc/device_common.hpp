@@ -101,7 +101,7 @@ __device__ __forceinline__ float gelu_erf(float x) {
     const float a1 = 0.254829592f, a2 = -0.284496736f, a3 = 1.421413741f,
                 a4 = -1.453152027f, a5 = 1.061405429f;
     float z = fabsf(x) * 0.70710678118654752f;
-    float t = 1.0f / (1.0f + p * z);
+    float t = __builtin_amdgcn_rcpf(1.0f + p * z);  // 1 ulp; 1 + p z >= 1, no denormals
     float poly = t * (a1 + t * (a2 + t * (a3 + t * (a4 + t * a5))));
     float q = 0.5f * poly * __expf(-z * z);
     return x * (x >= 0.0f ? 1.0f - q : q);
