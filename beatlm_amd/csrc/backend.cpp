@@ -1171,6 +1171,14 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                     ga.stages = fmath == Math::F16 && gk >= 2048 ? 3 : 2;
                     if (fmath == Math::F16) chosen = (gn <= 1024 && gk <= 1024 && rows <= 2048) ? TILE_32x64 : TILE_64x64;
                     else chosen = (gn >= 1024 && w64 <= 2ull * ctx->compute_units) ? TILE_64x64 : TILE_32x64;
+                    // bf16x3 outputs of whole 96-column tiles, at least 1536
+                    // wide, that fit one round at two 64 x 96 workgroups per CU
+                    // (fc1 at the encoder's sizes: 13.3 -> 12.3 us against 32 x
+                    // 64 in two rounds; QKV's 1152 columns measured slower
+                    // than its 64 x 64 tiles, 11.3 -> 12.1).
+                    if (fmath == Math::SPLIT && gn >= 1536 && gn % 96 == 0 &&
+                        wgs_of(TILE_64x96) <= 2ull * ctx->compute_units && !getenv("BL_GEMM_NO_96"))
+                        chosen = TILE_64x96;
                 }
                 if (const char *force = getenv("BL_GEMM_TILE")) {
                     int t = atoi(force);

@@ -233,9 +233,9 @@ hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
 hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s);
 
 // GEMM tile shapes the dispatcher can pick from: BM x BN.
-enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_128x32 = 4, TILE_COUNT = 5 };
-inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128}; return r[t]; }
-inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64, 32}; return c[t]; }
+enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_128x32 = 4, TILE_64x96 = 5, TILE_COUNT = 6 };
+inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128, 64}; return r[t]; }
+inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64, 32, 96}; return c[t]; }
 // K and N of a packed B are padded to these.
 constexpr uint32_t PACK_K = 32, PACK_N = 128;
 
