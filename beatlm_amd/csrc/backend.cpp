@@ -727,14 +727,16 @@ bl_binding resolve(const bl_spec &s, uint32_t b, const bl_binding_set &set) {
 // LayerNorms folded into the products that read them. A LayerNorm L (no
 // epilogue, whole) over x [rows][D] whose output n is internal and read by
 // nothing but one later product G, as G's A (G whole, the ring kernel, plain
-// rows, k = D, D a multiple of 32), while x was last written by a product P
-// before L (whole, no split k, its output exactly x, whole 32-column blocks
-// per wave) and nothing writes x between L and G:
+// rows, k = D, D a multiple of 32), while x was last written before L by a
+// product P (whole, no split k, its output exactly x, whole 32-column blocks
+// per wave) or by the class-token prepend (whole, the token whole blocks), and
+// nothing writes x between L and G:
 //   LN(x) W + b = rstd (x (gamma W) - mean c) + d,  c = column sums of gamma W,
 //   d = beta W + b,
 // so G reads x itself (its bf16 planes for bf16x3) with a pack of gamma W and
-// applies mean and rstd per row in its epilogue; P's epilogue leaves each
-// row's 32-column block statistics (and the planes). L launches nothing.
+// applies mean and rstd per row in its epilogue; P (its epilogue, or the
+// prepend's stats kernel) leaves each row's 32-column block statistics (and
+// the planes). L launches nothing.
 void plan_folds(bl_kernels *ks, const bl_spec *specs, uint32_t n, const bl_binding_set *sets, uint32_t n_sets,
                 const uint32_t *internal, uint32_t n_internal) {
     if (!n_internal || getenv("BL_NO_LN_FOLD")) return;
@@ -797,10 +799,23 @@ void plan_folds(bl_kernels *ks, const bl_spec *specs, uint32_t n, const bl_bindi
             pi = p;
             const Launch &P = ks->kernels[p].per_set[si];
             const bl_spec &ps = specs[p];
-            if (P.family != Family::GEMM || ps.part.count != 1 || P.gemm.ksplit > 1 || P.gemm.flash_ops || P.gemm.c_planes ||
-                P.out_lo != x_lo || P.out_hi != x_hi || P.gemm.n != D || P.gemm.m != ls.dims[0] || P.gemm.row0 != 0 ||
-                P.gemm.row1 != P.gemm.m || (gemm_tile_cols(P.tile) / 2) % 32 != 0 || P.math != G.math)
+            if (P.family == Family::ELEMENT) {
+                // The class-token prepend writing all of x (its token whole blocks).
+                // Its stats kernel loads and stores 16 bytes at a time.
+                auto a16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+                bool al = a16(P.el.a) && a16(P.el.b) && a16(P.el.y);
+                for (int k = 0; k < P.el.epi.n; k++)
+                    if (P.el.epi.kind[k] == BL_EPI_ADD) al = al && a16(P.el.epi.operand[k]);
+                if (P.element != PerElement::PREPEND || ps.part.count != 1 || P.out_lo != x_lo || P.out_hi != x_hi ||
+                    P.el.start != 0 || P.el.end != (uint64_t)ls.dims[0] * D || P.el.channels % 32 != 0 || P.f16 != G.f16 ||
+                    !al)
+                    ok = false;
+            } else if (P.family != Family::GEMM || ps.part.count != 1 || P.gemm.ksplit > 1 || P.gemm.flash_ops ||
+                       P.gemm.c_planes || P.out_lo != x_lo || P.out_hi != x_hi || P.gemm.n != D ||
+                       P.gemm.m != ls.dims[0] || P.gemm.row0 != 0 || P.gemm.row1 != P.gemm.m ||
+                       (gemm_tile_cols(P.tile) / 2) % 32 != 0 || P.math != G.math) {
                 ok = false;
+            }
         }
         if (!ok || pi < 0) continue;
         const uint32_t f = (uint32_t)ks->folds.size();
@@ -877,8 +892,15 @@ void apply_folds(bl_kernels *ks) {
             const Launch &Ln = ks->kernels[f.ln].per_set[si];
             const LnStatsArgs &sa = f.stats[si];
             const Pack &pk = ks->packs[G.pack];
-            P.gemm.ln_out = sa.stats;
-            P.gemm.ln_shadow = sa.shadow;
+            if (P.family == Family::ELEMENT) {
+                P.el.ln_out = sa.stats;
+                P.el.ln_shadow = sa.shadow;
+                P.el.ln_cols = sa.cols;
+                P.el.ln_plane = (uint64_t)sa.rows * sa.cols;
+            } else {
+                P.gemm.ln_out = sa.stats;
+                P.gemm.ln_shadow = sa.shadow;
+            }
             G.gemm.a = sa.shadow ? sa.shadow : sa.x;
             G.gemm.a_planes = sa.shadow ? (uint64_t)sa.rows * sa.cols : 0;
             G.gemm.ln_stats = sa.stats;
@@ -1180,9 +1202,15 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                         wgs_of(TILE_64x96) <= 2ull * ctx->compute_units && !getenv("BL_GEMM_NO_96"))
                         chosen = TILE_64x96;
                 }
+                bool tile_forced = false;
                 if (const char *force = getenv("BL_GEMM_TILE")) {
-                    int t = atoi(force);
-                    if (t >= 0 && t < TILE_COUNT) chosen = t;
+                    // "t" for every product, "t@n" for the products n columns wide.
+                    const int t = atoi(force);
+                    const char *at = strchr(force, '@');
+                    if (t >= 0 && t < TILE_COUNT && (!at || (uint32_t)atoi(at + 1) == gn)) {
+                        chosen = t;
+                        tile_forced = true;
+                    }
                 }
                 if (const char *force = getenv("BL_GEMM_KGROUPS")) ga.kgroups = (uint32_t)atoi(force);
                 if (const char *force = getenv("BL_GEMM_STAGES")) ga.stages = (uint32_t)atoi(force);
@@ -1199,7 +1227,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 // Otherwise 32 x 64: a convolution's window loads wait longer than
                 // a plain row's, and the smaller tile's extra workgroups hide it
                 // (148 x 148 x 64 -> 64: 19.8 us against 24.6 with 64 x 64).
-                if (conv && !getenv("BL_GEMM_TILE"))
+                if (conv && !tile_forced)
                     chosen = gn <= 32 && wgs_of(TILE_128x32) >= ctx->compute_units ? TILE_128x32 : TILE_32x64;
                 ga.ksplit = 1;
                 if (conv && !getenv("BL_CONV_NO_SPLIT_K")) {

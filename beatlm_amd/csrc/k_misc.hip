@@ -349,6 +349,93 @@ __global__ __launch_bounds__(256) void element_kernel(ElementArgs a) {
     }
 }
 
+// The class-token prepend (with its epilogue) as the producer of a folded
+// LayerNorm over its output: eight consecutive elements of one row per
+// invocation, so that a quad of invocations is one 32-column block (rows of
+// ln_cols elements, a multiple of 32, and a part of whole rows: a block lies
+// in one row, and in the token or in the rows after it). Stores y, the
+// block's (mean, sum of squared deviations from that mean) of the values as
+// stored at ln_out [row][ln_cols / 32], and for f32 storage y once more as hi
+// and lo bf16 planes (ln_shadow, ln_plane elements apart).
+// Eight consecutive values v[e] of element i + e (i a multiple of 8) from
+// 16-byte loads, f32 or f16.
+template <typename T>
+__device__ __forceinline__ void load8(const T *p, float (&v)[8]) {
+    if constexpr (sizeof(T) == 4) {
+        const f32x4 x = *(const f32x4 *)p, y = *(const f32x4 *)(p + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[e] = x[e];
+            v[4 + e] = y[e];
+        }
+    } else {
+        const f16x8 x = *(const f16x8 *)p;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (float)x[e];
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void prepend_stats_kernel(ElementArgs a) {
+    const T *A = (const T *)a.a, *B = (const T *)a.b;
+    T *Y = (T *)a.y;
+    const uint64_t chunks = (a.end - a.start) / 8;  // a multiple of 4: whole rows of whole blocks
+    const uint32_t nblk = a.ln_cols / 32;
+    for (uint64_t c = (uint64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (uint64_t)gridDim.x * 256) {
+        const uint64_t i = a.start + 8 * c;
+        float v[8], s = 0.0f;
+        load8<T>(i < a.channels ? A + i : B + (i - a.channels), v);
+        // The epilogue step by step over the eight values; an added tensor
+        // as 16-byte loads.
+        for (int k = 0; k < a.epi.n; k++) {
+            if (a.epi.kind[k] == BL_EPI_ADD) {
+                float w[8];
+                load8<T>((const T *)a.epi.operand[k] + i, w);
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] += w[e];
+            } else {
+                EpilogueArgs one = a.epi;
+                one.n = 1;
+                one.kind[0] = a.epi.kind[k];
+                one.factor[0] = a.epi.factor[k];
+                one.channels[0] = a.epi.channels[k];
+                one.operand[0] = a.epi.operand[k];
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = apply_epilogue<T>(one, v[e], i + e);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            v[e] = to_f32(from_f32<T>(v[e]));  // as stored
+            s += v[e];
+        }
+        if constexpr (sizeof(T) == 4) {
+            *(f32x4 *)(Y + i) = f32x4{v[0], v[1], v[2], v[3]};
+            *(f32x4 *)(Y + i + 4) = f32x4{v[4], v[5], v[6], v[7]};
+            if (a.ln_shadow) {
+                bf16x8 hi, lo;
+                split8_bf16(v, hi, lo);
+                *(bf16x8 *)((__bf16 *)a.ln_shadow + i) = hi;
+                *(bf16x8 *)((__bf16 *)a.ln_shadow + a.ln_plane + i) = lo;
+            }
+        } else {
+            f16x8 w;
+#pragma unroll
+            for (int e = 0; e < 8; e++) w[e] = (_Float16)v[e];
+            *(f16x8 *)(Y + i) = w;
+        }
+        const float mean = quad_sum(s) * (1.0f / 32.0f);
+        float m2 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) m2 += (v[e] - mean) * (v[e] - mean);
+        m2 = quad_sum(m2);
+        if (c % 4 == 0) {
+            const uint64_t row = i / a.ln_cols;
+            *(f32x2 *)(a.ln_out + 2 * (row * nblk + (i % a.ln_cols) / 32)) = f32x2{mean, m2};
+        }
+    }
+}
+
 // ------------------------------------------------------------------------
 // The DPT head's gathers, V consecutive channels of one output pixel per
 // invocation (V = 4 when the channel count is a multiple of 4, else 1).
@@ -615,6 +702,23 @@ hipError_t launch_gather(const GatherArgs &a, Gather g, bool f16, hipStream_t s)
 
 hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s) {
     if (a.end <= a.start) return hipSuccess;
+    if (a.ln_out) {
+        // Whole rows of whole 32-column blocks, the token whole blocks too.
+        if (p != PerElement::PREPEND || a.ln_cols == 0 || a.ln_cols % 32 != 0 || a.start % a.ln_cols != 0 ||
+            a.end % a.ln_cols != 0 || a.channels % 32 != 0 || (!f16 && a.ln_shadow && !a.ln_plane))
+            return hipErrorInvalidValue;
+        // 16-byte loads and stores of eight elements.
+        auto aligned = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+        bool ok = aligned(a.a) && aligned(a.b) && aligned(a.y) && (!a.ln_shadow || aligned(a.ln_shadow));
+        for (int k = 0; k < a.epi.n; k++)
+            if (a.epi.kind[k] == BL_EPI_ADD) ok = ok && aligned(a.epi.operand[k]);
+        if (!ok) return hipErrorInvalidValue;
+        uint64_t blocks = ((a.end - a.start) / 8 + 255) / 256;
+        if (blocks > 65535) blocks = 65535;
+        if (f16) hipLaunchKernelGGL((prepend_stats_kernel<_Float16>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((prepend_stats_kernel<float>), dim3((uint32_t)blocks), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     uint64_t blocks = (a.end - a.start + 255) / 256;
     if (blocks > 65535) blocks = 65535;
     dim3 grid((uint32_t)blocks);

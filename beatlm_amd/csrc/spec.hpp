@@ -188,6 +188,14 @@ struct ElementArgs {
     uint64_t start, end;  // output elements of the part
     uint32_t channels;
     EpilogueArgs epi;
+    // The prepend as a folded LayerNorm's producer (GemmArgs::ln_out and
+    // ln_shadow mean the same): the output's rows are ln_cols elements, a
+    // multiple of 32, and the part is whole rows; ln_shadow's planes are
+    // ln_plane elements apart. Null: none.
+    float *ln_out = nullptr;
+    void *ln_shadow = nullptr;
+    uint32_t ln_cols = 0;
+    uint64_t ln_plane = 0;
 };
 
 // A product with at most 4 output columns (the depth head's 1x1 convolution

@@ -178,3 +178,80 @@ def test_a_layernorm_whose_input_no_product_wrote_is_not_folded(ctx):
         assert not any("folded" in s for s in labels), labels
     finally:
         prep.close()
+
+
+# tensor ids of the prepend program below
+TOK, PAT, POS = 20, 21, 22
+XP = 23
+
+
+def prepend_graph(t=T, d=D, m=M):
+    """x = prepend(token, patches) + pos (the class token and position add of
+    the embeddings: the fold's producer), n = LN(x), out = GELU(n W1 + b1)."""
+    g = ir.Graph()
+    g.tensor(PAT, ir.INPUT, (t - 1) * d)
+    for tid, n in [(TOK, d), (POS, t * d), (G2, d), (B2, d), (W1, d * m), (B1, m)]:
+        g.tensor(tid, ir.WEIGHT, n)
+    g.tensor(30, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_PREPEND_TOKEN, [TOK, PAT], [t - 1, d]), 30)
+    g.tensor(XP, ir.OUTPUT, t * d)
+    g.push(ir.op(ir.OP_ADD, [30, POS], [t * d]), XP)
+    g.tensor(N2, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_LAYER_NORM, [XP, G2, B2], [t, d], EPS), N2)
+    g.tensor(H, ir.ACTIVATION, t * m)
+    g.push(ir.op(ir.OP_MATMUL, [N2, W1, B1], [t, d, m]), H)
+    g.tensor(OUT, ir.OUTPUT, t * m)
+    g.push(ir.op(ir.OP_GELU_ERF, [H], [t * m]), OUT)
+    return g
+
+
+def prepend_values(f16=False, seed=9):
+    v = values(seed=seed, f16=f16)
+    dt = np.float16 if f16 else np.float32
+    rng = np.random.default_rng(seed + 1)
+    v[TOK] = rng.uniform(-1, 1, D).astype(dt)
+    v[PAT] = rng.uniform(-2, 2, (T - 1) * D).astype(dt)
+    v[POS] = rng.uniform(-0.5, 0.5, T * D).astype(dt)
+    return {k: a for k, a in v.items() if k in (TOK, PAT, POS, G2, B2, W1, B1)}
+
+
+@pytest.mark.parametrize("dtype", [hip.F32, hip.F16])
+def test_the_class_token_prepend_leaves_the_statistics_of_a_folded_layernorm(ctx, dtype):
+    """The prepend (with its position add) writes x, its block statistics and,
+    for bf16x3, x's planes: the LayerNorm launches nothing, and the product
+    after it matches the oracle's prepend, add, LayerNorm, matmul and GELU;
+    the same after the host rewrites x and the reader is encoded alone."""
+    f16 = dtype == hip.F16
+    prep = ir.prepare(ctx, prepend_graph(), dtype=dtype)
+    try:
+        labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+        assert "row statistics" in labels[0] and "folded into 2" in labels[1] and "< layernorm 1" in labels[2], labels
+        v = prepend_values(f16)
+        for tid, a in v.items():
+            prep.write(tid, a)
+        prep.run()
+        ctx.synchronize()
+        assert prep.kernels.range_launches(0, 3) == 2
+        v32 = {k: a.astype(np.float32) for k, a in v.items()}
+        want_x = oracle.add(oracle.prepend_token(v32[TOK], v32[PAT], T - 1, D), v32[POS])
+        x = prep.read(XP).astype(np.float32)
+        if f16:
+            assert np.array_equal(x, want_x.astype(np.float16).astype(np.float32))
+            err = float(np.max(np.abs(prep.read(OUT).astype(np.float32) - want_out(x, v32))))
+            print(f"prepend as the fold's producer, f16 storage: max abs error {err:.3e}")
+            assert err <= 2e-2
+            return
+        assert np.array_equal(x, want_x)
+        assert_close(prep.read(OUT), want_out(x, v), "prepend as the fold's producer")
+        st = prep.kernels.fold_read(0, 0, T * (D // 32) * 2).reshape(T, D // 32, 2).astype(np.float64)
+        blocks = x.astype(np.float64).reshape(T, D // 32, 32)
+        mean = blocks.mean(2)
+        np.testing.assert_allclose(st[:, :, 0], mean, atol=1e-6)
+        np.testing.assert_allclose(st[:, :, 1], ((blocks - mean[:, :, None]) ** 2).sum(2), rtol=1e-5, atol=1e-5)
+        x2 = oracle.uniform(77, T * D, -3.0, 3.0)
+        prep.write(XP, x2)
+        prep.kernels.encode(2)
+        ctx.synchronize()
+        assert_close(prep.read(OUT), want_out(x2, v), "the reader alone after a host write of x")
+    finally:
+        prep.close()
