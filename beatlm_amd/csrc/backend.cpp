@@ -359,6 +359,9 @@ struct Launch {
     // statistics from x when the producer has not written them since x changed.
     int fold = -1;
     int fold_role = 0;
+    // A class-token prepend fused into the patch embedding before it: it
+    // launches nothing (the product writes its output).
+    bool fused = false;
 };
 enum FoldRole : int { FOLD_NONE = 0, FOLD_LAYER_NORM = 1, FOLD_CONSUMER = 2, FOLD_PRODUCER = 3 };
 
@@ -724,6 +727,74 @@ bl_binding resolve(const bl_spec &s, uint32_t b, const bl_binding_set &set) {
     return bd;
 }
 
+// The class-token prepend fused into the patch embedding that makes its rows
+// (the embeddings' x = [token; patches] + pos): a prepend Q (whole) whose rows
+// are an internal tensor written by nothing but the patch embedding P just
+// before it (whole, no epilogue, not split) and read by nothing but Q. P then
+// writes x's rows 1 .. m itself through Q's epilogue (its added tensors read
+// one row on), its first row band also writes x's first row from the token,
+// and Q launches nothing. Q's epilogue steps must not depend on where a row
+// lies: adds of x-shaped tensors, scales, activations, channel scales over a
+// divisor of the row.
+void plan_prepends(bl_kernels *ks, const bl_spec *specs, uint32_t n, const uint32_t *internal, uint32_t n_internal) {
+    if (!n_internal || getenv("BL_NO_PREPEND_FUSION")) return;
+    std::vector<uint32_t> ids(internal, internal + n_internal);
+    std::sort(ids.begin(), ids.end());
+    for (uint32_t qi = 1; qi < n; qi++) {
+        const bl_spec &qs = specs[qi];
+        const uint32_t pi = qi - 1;
+        const bl_spec &ps = specs[pi];
+        if (qs.main != BL_MAIN_PREPEND_TOKEN || qs.part.count != 1 || ps.main != BL_MAIN_PATCH_EMBED ||
+            ps.part.count != 1 || ps.n_epilogue)
+            continue;
+        const uint32_t rows_t = qs.bindings[qs.reads[1]].tensor;
+        if (!std::binary_search(ids.begin(), ids.end(), rows_t) || ps.bindings[ps.n_bindings - 1].tensor != rows_t) continue;
+        bool ok = true;
+        for (uint32_t ki = 0; ki < n && ok; ki++) {
+            const bl_spec &s = specs[ki];
+            const uint32_t last = s.n_bindings - 1;
+            if (ki != pi && s.bindings[last].tensor == rows_t) ok = false;
+            for (uint32_t b = 0; b < last; b++)
+                if (s.bindings[b].tensor == rows_t && !(ki == qi && b == qs.reads[1])) ok = false;
+        }
+        for (uint32_t si = 0; si < ks->sets && ok; si++) {
+            const Launch &P = ks->kernels[pi].per_set[si];
+            const Launch &Q = ks->kernels[qi].per_set[si];
+            const GemmArgs &g = P.gemm;
+            ok = P.family == Family::GEMM && Q.family == Family::ELEMENT && Q.element == PerElement::PREPEND &&
+                 g.load == 2 && g.ksplit <= 1 && !g.flash_ops && !g.c_planes && g.epi_mode == 0 && g.row0 == 0 &&
+                 g.row1 == g.m && g.n == Q.el.channels && Q.el.start == 0 &&
+                 Q.el.end == (uint64_t)(g.m + 1) * g.n && P.out_lo == (const char *)Q.el.b && P.f16 == Q.f16;
+            for (int k = 0; k < Q.el.epi.n && ok; k++) {
+                const int kind = Q.el.epi.kind[k];
+                ok = kind == BL_EPI_ADD || kind == BL_EPI_RELU || kind == BL_EPI_GELU || kind == BL_EPI_GELU_ERF ||
+                     kind == BL_EPI_SCALE || (kind == BL_EPI_CHANNEL_SCALE && Q.el.epi.channels[k] && g.n % Q.el.epi.channels[k] == 0);
+            }
+        }
+        if (!ok) continue;
+        for (uint32_t si = 0; si < ks->sets; si++) {
+            Launch &P = ks->kernels[pi].per_set[si];
+            Launch &Q = ks->kernels[qi].per_set[si];
+            GemmArgs &g = P.gemm;
+            const uint64_t row_bytes = (uint64_t)g.n * (P.f16 ? 2 : 4);
+            g.c = (char *)Q.el.y + row_bytes;
+            g.epi = Q.el.epi;
+            for (int k = 0; k < g.epi.n; k++)
+                if (g.epi.kind[k] == BL_EPI_ADD) g.epi.operand[k] = (const char *)g.epi.operand[k] + row_bytes;
+            g.epi_mode = 3;
+            g.cls_token = Q.el.a;
+            g.cls_out = Q.el.y;
+            g.cls_epi = Q.el.epi;
+            P.out_lo = Q.out_lo;
+            P.out_hi = Q.out_hi;
+            Q.fused = true;
+            Q.out_lo = Q.out_hi = nullptr;
+        }
+        ks->kernels[qi].label += " > fused into " + std::to_string(pi);
+        ks->kernels[pi].label += " < prepend " + std::to_string(qi);
+    }
+}
+
 // LayerNorms folded into the products that read them. A LayerNorm L (no
 // epilogue, whole) over x [rows][D] whose output n is internal and read by
 // nothing but one later product G, as G's A (G whole, the ring kernel, plain
@@ -812,7 +883,7 @@ void plan_folds(bl_kernels *ks, const bl_spec *specs, uint32_t n, const bl_bindi
                     ok = false;
             } else if (P.family != Family::GEMM || ps.part.count != 1 || P.gemm.ksplit > 1 || P.gemm.flash_ops ||
                        P.gemm.c_planes || P.out_lo != x_lo || P.out_hi != x_hi || P.gemm.n != D ||
-                       P.gemm.m != ls.dims[0] || P.gemm.row0 != 0 || P.gemm.row1 != P.gemm.m ||
+                       P.gemm.m + (P.gemm.cls_out ? 1 : 0) != ls.dims[0] || P.gemm.row0 != 0 || P.gemm.row1 != P.gemm.m ||
                        (gemm_tile_cols(P.tile) / 2) % 32 != 0 || P.math != G.math) {
                 ok = false;
             }
@@ -897,6 +968,13 @@ void apply_folds(bl_kernels *ks) {
                 P.el.ln_shadow = sa.shadow;
                 P.el.ln_cols = sa.cols;
                 P.el.ln_plane = (uint64_t)sa.rows * sa.cols;
+            } else if (P.gemm.cls_out) {
+                // The product's rows are x's rows 1 .. m; its first row band writes row 0.
+                P.gemm.ln_out = sa.stats + 2 * (sa.cols / 32);
+                P.gemm.ln_shadow = sa.shadow ? (char *)sa.shadow + (uint64_t)sa.cols * 2 : nullptr;
+                P.gemm.ln_plane = (uint64_t)sa.rows * sa.cols;
+                P.gemm.cls_ln_out = sa.stats;
+                P.gemm.cls_shadow = sa.shadow;
             } else {
                 P.gemm.ln_out = sa.stats;
                 P.gemm.ln_shadow = sa.shadow;
@@ -1351,6 +1429,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
         }
         ks->kernels.push_back(std::move(k));
     }
+    plan_prepends(ks, specs, n, internal, n_internal);
     plan_folds(ks, specs, n, sets, n_sets, internal, n_internal);
     // The backend's own device memory, one allocation beside the plan's
     // arenas: the packed weights, then the split-k GEMMs' partial sums, then
@@ -1530,6 +1609,7 @@ static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
 }
 
 static hipError_t launch(const Launch &L, hipStream_t s) {
+    if (L.fused) return hipSuccess;  // the product before it does its work
     switch (L.family) {
     case Family::LAYER_NORM: return L.fold_role == FOLD_LAYER_NORM ? hipSuccess : launch_layernorm(L.ln, L.f16, s);
     case Family::GEMM: {
@@ -1598,6 +1678,7 @@ static Launch with_kv(const Launch &L, uint32_t i, KvState &kv) {
 static hipError_t run_one(bl_kernels *k, uint32_t i, uint32_t set, hipStream_t s, KvState &kv, FoldState &fs) {
     const Launch &L = k->kernels[i].per_set[set];
     const uint32_t sets = k->sets;
+    if (L.fused) return hipSuccess;
     if (L.fold >= 0 && (L.fold_role == FOLD_LAYER_NORM || L.fold_role == FOLD_CONSUMER)) {
         const size_t at = (size_t)L.fold * sets + set;
         if (!fs.valid[at]) {

@@ -87,6 +87,20 @@ struct GemmArgs {
     float ln_eps;
     // The ring kernel's per-lane epilogue in place of the one through LDS.
     uint32_t lane_epilogue;
+    // ln_shadow's plane distance in elements (0: m * n).
+    uint64_t ln_plane;
+    // The class-token prepend fused into this product (a patch embedding,
+    // the plain kernel): c is x's second row, so that the product's rows are
+    // x's rows 1 .. m, and the epilogue's added tensors are read one row on
+    // likewise; the workgroups of the first row band also write x's first
+    // row, cls_epi applied to cls_token [n], at cls_out (x itself), with its
+    // block statistics at cls_ln_out and its planes at cls_shadow when the
+    // product is a fold's producer. Null cls_out: none.
+    const void *cls_token;
+    void *cls_out;
+    float *cls_ln_out;
+    void *cls_shadow;
+    EpilogueArgs cls_epi;
 };
 
 hipError_t launch_gemm_reduce(const GemmArgs &a, bool f16, hipStream_t s);

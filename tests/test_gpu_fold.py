@@ -255,3 +255,94 @@ def test_the_class_token_prepend_leaves_the_statistics_of_a_folded_layernorm(ctx
         assert_close(prep.read(OUT), want_out(x2, v), "the reader alone after a host write of x")
     finally:
         prep.close()
+
+
+# tensor ids of the embeddings program below
+IMG, PW, PB = 40, 41, 42
+
+
+def embeddings_graph(grid, d, m, fold=True):
+    """patches = patch_embed(image), x = prepend(token, patches) + pos (the
+    prepend fused into the patch embedding), then n = LN(x) and out =
+    GELU(n W1 + b1) (the LayerNorm folded, the patch embedding its producer)."""
+    t = grid * grid + 1
+    g = ir.Graph()
+    g.tensor(IMG, ir.INPUT, (grid * 14) ** 2 * 3)
+    for tid, n in [(PW, 14 * 14 * 3 * d), (PB, d), (TOK, d), (POS, t * d), (G2, d), (B2, d), (W1, d * m), (B1, m)]:
+        g.tensor(tid, ir.WEIGHT, n)
+    g.tensor(31, ir.ACTIVATION, (t - 1) * d)
+    g.push(ir.op(ir.OP_PATCH_EMBED, [IMG, PW, PB], [grid, grid, 14, 3, d]), 31)
+    g.tensor(30, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_PREPEND_TOKEN, [TOK, 31], [t - 1, d]), 30)
+    g.tensor(XP, ir.OUTPUT, t * d)
+    g.push(ir.op(ir.OP_ADD, [30, POS], [t * d]), XP)
+    g.tensor(N2, ir.ACTIVATION, t * d)
+    g.push(ir.op(ir.OP_LAYER_NORM, [XP, G2, B2], [t, d], EPS), N2)
+    g.tensor(H, ir.ACTIVATION, t * m)
+    g.push(ir.op(ir.OP_MATMUL, [N2, W1, B1], [t, d, m]), H)
+    g.tensor(OUT, ir.OUTPUT, t * m)
+    g.push(ir.op(ir.OP_GELU_ERF, [H], [t * m]), OUT)
+    return g
+
+
+@pytest.mark.parametrize("grid,dtype", [(10, hip.F32), (37, hip.F32), (10, hip.F16)])
+def test_the_prepend_fused_into_the_patch_embedding_feeds_a_folded_layernorm(ctx, grid, dtype):
+    """The patch embedding writes x = [token; patches] + pos itself (the prepend
+    launches nothing) and x's row statistics and planes for the LayerNorm
+    folded into the product after it: two launches for the four kernels, x
+    and the product's output as the oracle's embeddings, LayerNorm, matmul
+    and GELU give them."""
+    d, m = 384, 512
+    t = grid * grid + 1
+    f16 = dtype == hip.F16
+    prep = ir.prepare(ctx, embeddings_graph(grid, d, m), dtype=dtype)
+    try:
+        labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+        assert "< prepend 1" in labels[0] and "row statistics" in labels[0], labels
+        assert "fused into 0" in labels[1] and "folded into 3" in labels[2], labels
+        dt = np.float16 if f16 else np.float32
+        rng = np.random.default_rng(grid)
+        v = {
+            IMG: rng.uniform(-2, 2, (grid * 14) ** 2 * 3).astype(dt),
+            PW: rng.uniform(-0.05, 0.05, 14 * 14 * 3 * d).astype(dt),
+            PB: rng.uniform(-0.1, 0.1, d).astype(dt),
+            TOK: rng.uniform(-1, 1, d).astype(dt),
+            POS: rng.uniform(-0.5, 0.5, t * d).astype(dt),
+            G2: (1 + 0.1 * rng.standard_normal(d)).astype(dt),
+            B2: (0.1 * rng.standard_normal(d)).astype(dt),
+            W1: rng.uniform(-0.05, 0.05, d * m).astype(dt),
+            B1: rng.uniform(-0.1, 0.1, m).astype(dt),
+        }
+        for tid, a in v.items():
+            prep.write(tid, a)
+        prep.run()
+        ctx.synchronize()
+        assert prep.kernels.range_launches(0, len(prep.kernels)) == 2
+        v32 = {k: a.astype(np.float32) for k, a in v.items()}
+        patches = oracle.patch_embed(v32[IMG], v32[PW], v32[PB], grid, grid, 14, 3, d)
+        want_x = oracle.add(oracle.prepend_token(v32[TOK], patches, t - 1, d), v32[POS])
+        x = prep.read(XP).astype(np.float32)
+        n = oracle.layernorm(x, v32[G2], v32[B2], t, d, EPS)
+        want = oracle.gelu_erf(oracle.matmul(n, v32[W1], v32[B1], t, d, m))
+        got = prep.read(OUT).astype(np.float32)
+        if f16:
+            ex = float(np.max(np.abs(x - want_x)))
+            eo = float(np.max(np.abs(got - want)))
+            print(f"prepend fused, f16 storage, grid {grid}: x {ex:.3e}, output {eo:.3e}")
+            assert ex <= 2e-2 and eo <= 2e-2
+            return
+        # The class row is exact; the patch rows are the product's.
+        assert np.array_equal(x[:d], want_x[:d])
+        # Timing the fused prepend on its own launches nothing, so x stays.
+        prep.kernels.time(1, 3)
+        ctx.synchronize()
+        assert np.array_equal(prep.read(XP), x)
+        assert_close(x, want_x, f"embeddings with the prepend fused, grid {grid}")
+        assert_close(got, want, f"the folded LayerNorm's product after the fused prepend, grid {grid}")
+        st = prep.kernels.fold_read(0, 0, t * (d // 32) * 2).reshape(t, d // 32, 2).astype(np.float64)
+        blocks = x.astype(np.float64).reshape(t, d // 32, 32)
+        mean = blocks.mean(2)
+        np.testing.assert_allclose(st[:, :, 0], mean, atol=1e-6)
+        np.testing.assert_allclose(st[:, :, 1], ((blocks - mean[:, :, None]) ** 2).sum(2), rtol=1e-5, atol=1e-5)
+    finally:
+        prep.close()
