@@ -290,7 +290,11 @@ const char *bl_kernels_label(const bl_kernels *kernels, uint32_t kernel);
  * projection's epilogue wrote into the backend's scratch reads them from
  * there only when nothing has written qkv since; otherwise (the kernel
  * encoded alone, a host write, another kernel over those bytes) it makes
- * them from qkv itself first. */
+ * them from qkv itself first. Kernels of bl_kernels_create_internal whose work
+ * another kernel does launch nothing: a LayerNorm folded into the product
+ * that reads it, and a class-token prepend fused into the patch embedding
+ * before it (which writes the prepend's output; the internal patches tensor
+ * between them is never written). */
 int bl_kernels_encode(bl_kernels *kernels, uint32_t kernel, uint32_t set,
                       bl_timer *timer, uint32_t tag);
 /* Launches kernels [first, first + count) in order with binding set `set`.
