@@ -402,6 +402,10 @@ struct Pack {
     }
 };
 
+// Bytes of a folded pack's column vectors: c [n_pad], d [n_pad], then the
+// per-block column sums cb [n_pad][32].
+inline uint64_t fold_vec_bytes(uint32_t n_pad) { return (uint64_t)(2 + 32) * n_pad * sizeof(float); }
+
 // One LayerNorm folded into the product that reads its output. Per binding
 // set: x's bytes (the LayerNorm's input) and the statistics launch that makes
 // the fold's buffers from x.
@@ -947,10 +951,10 @@ void plan_folds(bl_kernels *ks, const bl_spec *specs, uint32_t n, const bl_bindi
 }
 
 // Bytes of a fold's buffers for one binding set: the statistics, then (f32
-// storage in bf16x3) x's planes.
+// storage) x centred per block, as bf16 planes (bf16x3) or f32.
 uint64_t fold_stats_bytes(const Fold &f) { return (uint64_t)f.stats[0].rows * (f.stats[0].cols / 32) * 8; }
 uint64_t fold_plane_bytes(const Fold &f, const Launch &G) {
-    return G.math == Math::SPLIT ? (uint64_t)f.stats[0].rows * f.stats[0].cols * 4 : 0;
+    return G.math != Math::F16 ? (uint64_t)f.stats[0].rows * f.stats[0].cols * 4 : 0;
 }
 
 // Points the folds' launches at their buffers (after the split activations
@@ -963,27 +967,32 @@ void apply_folds(bl_kernels *ks) {
             const Launch &Ln = ks->kernels[f.ln].per_set[si];
             const LnStatsArgs &sa = f.stats[si];
             const Pack &pk = ks->packs[G.pack];
+            // The shadow (f32 storage): x centred per block, as bf16 planes
+            // sa.planes elements apart (bf16x3) or as f32 (sa.planes 0).
+            const uint64_t shadow_elt = sa.planes ? 2 : 4;
             if (P.family == Family::ELEMENT) {
                 P.el.ln_out = sa.stats;
                 P.el.ln_shadow = sa.shadow;
                 P.el.ln_cols = sa.cols;
-                P.el.ln_plane = (uint64_t)sa.rows * sa.cols;
+                P.el.ln_plane = sa.planes;
             } else if (P.gemm.cls_out) {
                 // The product's rows are x's rows 1 .. m; its first row band writes row 0.
                 P.gemm.ln_out = sa.stats + 2 * (sa.cols / 32);
-                P.gemm.ln_shadow = sa.shadow ? (char *)sa.shadow + (uint64_t)sa.cols * 2 : nullptr;
-                P.gemm.ln_plane = (uint64_t)sa.rows * sa.cols;
+                P.gemm.ln_shadow = sa.shadow ? (char *)sa.shadow + (uint64_t)sa.cols * shadow_elt : nullptr;
+                P.gemm.ln_plane = sa.planes;
                 P.gemm.cls_ln_out = sa.stats;
                 P.gemm.cls_shadow = sa.shadow;
             } else {
                 P.gemm.ln_out = sa.stats;
                 P.gemm.ln_shadow = sa.shadow;
+                P.gemm.ln_plane = sa.planes;
             }
             G.gemm.a = sa.shadow ? sa.shadow : sa.x;
-            G.gemm.a_planes = sa.shadow ? (uint64_t)sa.rows * sa.cols : 0;
+            G.gemm.a_planes = sa.shadow ? sa.planes : 0;
             G.gemm.ln_stats = sa.stats;
             G.gemm.ln_c = (const float *)((char *)ks->pack_buffer + pk.vec_offset);
             G.gemm.ln_d = G.gemm.ln_c + pk.n_pad;
+            G.gemm.ln_cb = sa.shadow ? G.gemm.ln_c + 2 * (uint64_t)pk.n_pad : nullptr;
             G.gemm.ln_blocks = sa.cols / 32;
             G.gemm.ln_eps = Ln.ln.eps;
             G.gemm.bias = nullptr;
@@ -1446,7 +1455,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
         pack_total += align256(packed_bytes(pk.math, pk.k_pad, pk.n_pad));
         if (pk.folded()) {
             pk.vec_offset = pack_total;
-            pack_total += align256((uint64_t)2 * pk.n_pad * sizeof(float));
+            pack_total += align256(fold_vec_bytes(pk.n_pad));
         }
         // Written by a kernel of this program: packed again before every launch.
         for (uint32_t ki = 0; ki < n && !pk.dynamic; ki++) {
@@ -1533,8 +1542,10 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 LnStatsArgs &sa = f.stats[si];
                 sa.stats = (float *)(ks->workspace + at);
                 at += align256(fold_stats_bytes(f));
-                const uint64_t planes = fold_plane_bytes(f, ks->kernels[f.consumer].per_set[si]);
+                const Launch &G = ks->kernels[f.consumer].per_set[si];
+                const uint64_t planes = fold_plane_bytes(f, G);
                 sa.shadow = planes ? ks->workspace + at : nullptr;
+                sa.planes = planes && G.math == Math::SPLIT ? (uint64_t)sa.rows * sa.cols : 0;
                 at += align256(planes);
             }
         apply_folds(ks);
@@ -1564,7 +1575,9 @@ extern "C" void bl_kernels_destroy(bl_kernels *k) {
 extern "C" uint64_t bl_kernels_packs_made(const bl_kernels *k) { return k ? k->packs_made : 0; }
 
 // Test hook: a fold's device buffers copied out (synchronously): what = 0 its
-// statistics for binding set `set`, 1 the column vectors c then d of its pack.
+// statistics for binding set `set`, 1 the column vectors of its pack (c, d,
+// then the per-block column sums [n_pad][32]), 2 its shadow (x centred per
+// block) for binding set `set`.
 extern "C" int bl_kernels_fold_read(bl_kernels *k, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes) {
     if (!k || !dst || fold >= k->folds.size() || set >= k->sets) return BL_ERR_INVALID_ARGUMENT;
     const Fold &f = k->folds[fold];
@@ -1574,10 +1587,13 @@ extern "C" int bl_kernels_fold_read(bl_kernels *k, uint32_t fold, uint32_t set, 
     if (what == 0) {
         src = f.stats[set].stats;
         have = fold_stats_bytes(f);
+    } else if (what == 2) {
+        src = f.stats[set].shadow;
+        have = src ? fold_plane_bytes(f, G) : 0;
     } else {
         const Pack &pk = k->packs[G.pack];
         src = (const char *)k->pack_buffer + pk.vec_offset;
-        have = (uint64_t)2 * pk.n_pad * sizeof(float);
+        have = fold_vec_bytes(pk.n_pad);
     }
     if (bytes > have) return BL_ERR_INVALID_ARGUMENT;
     hipSetDevice(k->ctx->device);

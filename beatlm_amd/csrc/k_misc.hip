@@ -356,7 +356,8 @@ __global__ __launch_bounds__(256) void element_kernel(ElementArgs a) {
 // in one row, and in the token or in the rows after it). Stores y, the
 // block's (mean, sum of squared deviations from that mean) of the values as
 // stored at ln_out [row][ln_cols / 32], and for f32 storage y once more as hi
-// and lo bf16 planes (ln_shadow, ln_plane elements apart).
+// and lo bf16 planes (ln_shadow, ln_plane elements apart) or as f32
+// (ln_plane 0), each value less its block's mean.
 // Eight consecutive values v[e] of element i + e (i a multiple of 8) from
 // 16-byte loads, f32 or f16.
 template <typename T>
@@ -412,12 +413,6 @@ __global__ __launch_bounds__(256) void prepend_stats_kernel(ElementArgs a) {
         if constexpr (sizeof(T) == 4) {
             *(f32x4 *)(Y + i) = f32x4{v[0], v[1], v[2], v[3]};
             *(f32x4 *)(Y + i + 4) = f32x4{v[4], v[5], v[6], v[7]};
-            if (a.ln_shadow) {
-                bf16x8 hi, lo;
-                split8_bf16(v, hi, lo);
-                *(bf16x8 *)((__bf16 *)a.ln_shadow + i) = hi;
-                *(bf16x8 *)((__bf16 *)a.ln_shadow + a.ln_plane + i) = lo;
-            }
         } else {
             f16x8 w;
 #pragma unroll
@@ -432,6 +427,23 @@ __global__ __launch_bounds__(256) void prepend_stats_kernel(ElementArgs a) {
         if (c % 4 == 0) {
             const uint64_t row = i / a.ln_cols;
             *(f32x2 *)(a.ln_out + 2 * (row * nblk + (i % a.ln_cols) / 32)) = f32x2{mean, m2};
+        }
+        if constexpr (sizeof(T) == 4) {
+            if (a.ln_shadow) {
+                // The consumer's A: the values less their block's mean.
+                float dv[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) dv[e] = v[e] - mean;
+                if (a.ln_plane) {
+                    bf16x8 hi, lo;
+                    split8_bf16(dv, hi, lo);
+                    *(bf16x8 *)((__bf16 *)a.ln_shadow + i) = hi;
+                    *(bf16x8 *)((__bf16 *)a.ln_shadow + a.ln_plane + i) = lo;
+                } else {
+                    *(f32x4 *)((float *)a.ln_shadow + i) = f32x4{dv[0], dv[1], dv[2], dv[3]};
+                    *(f32x4 *)((float *)a.ln_shadow + i + 4) = f32x4{dv[4], dv[5], dv[6], dv[7]};
+                }
+            }
         }
     }
 }
@@ -631,7 +643,8 @@ __global__ void spin_kernel(uint64_t ticks) {
 // A folded LayerNorm's statistics of x made from x itself: one invocation
 // per (row, 32-column block), the block's mean and then its sum of squared
 // deviations from it, as the fold's producer computes them in its epilogue;
-// f32 x also goes to the shadow's hi and lo bf16 planes (rows * cols apart).
+// f32 x also goes to the shadow less its block's mean, as hi and lo bf16
+// planes (a.planes apart) or as f32 (a.planes 0).
 template <typename T>
 __global__ __launch_bounds__(256) void ln_stats_kernel(LnStatsArgs a) {
     const uint32_t nblk = a.cols / 32;
@@ -654,10 +667,10 @@ __global__ __launch_bounds__(256) void ln_stats_kernel(LnStatsArgs a) {
     *(f32x2 *)(a.stats + 2 * i) = f32x2{mean, sq};
     if constexpr (sizeof(T) == 4) {
         if (a.shadow) {
-            const uint64_t planes = (uint64_t)a.rows * a.cols;
 #pragma unroll
             for (int e = 0; e < 32; e += 4)
-                store_f32x4((float *)a.shadow, base + e, f32x4{v[e], v[e + 1], v[e + 2], v[e + 3]}, planes);
+                store_f32x4((float *)a.shadow, base + e,
+                            f32x4{v[e] - mean, v[e + 1] - mean, v[e + 2] - mean, v[e + 3] - mean}, a.planes);
         }
     }
 }
@@ -705,7 +718,7 @@ hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStrea
     if (a.ln_out) {
         // Whole rows of whole 32-column blocks, the token whole blocks too.
         if (p != PerElement::PREPEND || a.ln_cols == 0 || a.ln_cols % 32 != 0 || a.start % a.ln_cols != 0 ||
-            a.end % a.ln_cols != 0 || a.channels % 32 != 0 || (!f16 && a.ln_shadow && !a.ln_plane))
+            a.end % a.ln_cols != 0 || a.channels % 32 != 0)
             return hipErrorInvalidValue;
         // 16-byte loads and stores of eight elements.
         auto aligned = [](const void *q) { return ((uintptr_t)q & 15) == 0; };

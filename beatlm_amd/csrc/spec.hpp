@@ -72,17 +72,23 @@ struct GemmArgs {
     // A LayerNorm over this product's output folded into the product that
     // reads the LayerNorm's output (this product is the fold's producer):
     // ln_out [m][n / 32] of (mean, sum of squared deviations from that mean)
-    // of each row's 32-column blocks of the output as stored; ln_shadow
-    // (bf16x3) the output once more as hi and lo bf16 planes m * n elements
-    // apart, the consumer's A. Null: none.
+    // of each row's 32-column blocks of the output as stored; ln_shadow (f32
+    // storage) the output once more, centred per block (each value less its
+    // block's mean), as hi and lo bf16 planes m * n elements apart for
+    // bf16x3 or as f32 for the f32 matrix cores: the consumer's A. Null: none.
     float *ln_out;
     void *ln_shadow;
     // A LayerNorm folded into this product (the fold's consumer): A is the
-    // LayerNorm's input x (its bf16 planes for bf16x3); ln_stats holds x's
-    // block statistics as ln_out does; the packed B holds gamma (.) B row by
-    // row, ln_c [n] its column sums and ln_d [n] = beta . B[:, n] + bias[n],
-    // so that LN(x) B + bias = rstd (x (gamma B) - mean c) + d.
-    const float *ln_stats, *ln_c, *ln_d;
+    // LayerNorm's input x; ln_stats holds x's block statistics as ln_out
+    // does; the packed B holds gamma (.) B row by row, ln_c [n] its column
+    // sums and ln_d [n] = beta . B[:, n] + bias[n], so that
+    // LN(x) B + bias = rstd (x (gamma B) - mean c) + d (f16 storage). With
+    // ln_cb (f32 storage) A is x centred per block (the producer's shadow) and
+    // ln_cb [n][32] holds the column sums of gamma (.) B over each 32-row
+    // block of k: LN(x) B + bias = rstd (A (gamma B) + sum_b (mean_b - mean)
+    // cb[b]) + d, where the correction is one more product on the matrix cores
+    // and no term carries x's common offset.
+    const float *ln_stats, *ln_c, *ln_d, *ln_cb;
     uint32_t ln_blocks;   // 32-column blocks of x (k / 32)
     float ln_eps;
     // The ring kernel's per-lane epilogue in place of the one through LDS.
@@ -121,12 +127,14 @@ struct PackArgs {
 // A folded LayerNorm's statistics made from x itself (when the fold's
 // producer has not written them since x last changed): x [rows][cols]
 // (cols a multiple of 32) -> stats [rows][cols / 32] of (mean, sum of squared
-// deviations), and (f32 x, shadow non-null) x as hi and lo bf16 planes.
+// deviations), and (f32 x, shadow non-null) x centred per block, as hi and
+// lo bf16 planes `planes` elements apart, or as f32 (planes 0).
 struct LnStatsArgs {
     const void *x;
     float *stats;
     void *shadow;
     uint32_t rows, cols;
+    uint64_t planes;
 };
 hipError_t launch_ln_stats(const LnStatsArgs &a, bool f16, hipStream_t s);
 
@@ -205,7 +213,7 @@ struct ElementArgs {
     // The prepend as a folded LayerNorm's producer (GemmArgs::ln_out and
     // ln_shadow mean the same): the output's rows are ln_cols elements, a
     // multiple of 32, and the part is whole rows; ln_shadow's planes are
-    // ln_plane elements apart. Null: none.
+    // ln_plane elements apart (0: the shadow is f32). Null: none.
     float *ln_out = nullptr;
     void *ln_shadow = nullptr;
     uint32_t ln_cols = 0;

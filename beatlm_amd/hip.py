@@ -410,7 +410,8 @@ class Kernels:
 
     def fold_read(self, fold: int, what: int, floats: int, set_index: int = 0) -> np.ndarray:
         """A folded LayerNorm's buffers: what = 0 the statistics, 1 the column
-        vectors c then d (diagnostics)."""
+        vectors c, d and the per-block column sums, 2 the centred shadow of x
+        (diagnostics; `floats` counts 4-byte words)."""
         out = np.zeros(floats, np.float32)
         self.ctx.check(
             self.ctx._lib.bl_kernels_fold_read(self.handle, fold, set_index, what, out.ctypes.data_as(C.c_void_p), out.nbytes)

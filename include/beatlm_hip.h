@@ -325,15 +325,21 @@ uint64_t bl_kernels_packs_made(const bl_kernels *kernels);
 uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
 /* A LayerNorm whose output only a later product reads, as its A, while its
  * input x was last written by an earlier product, is folded into the reader:
- * LN(x) W + b = rstd (x (gamma W) - mean c) + d with c the column sums of
- * gamma W and d = beta W + b, the writer of x leaving each row's 32-column
- * block statistics (mean, sum of squared deviations) and the LayerNorm
- * launching nothing. bl_kernels_fold_read copies fold `fold`'s device
- * buffers out after waiting for the stream: what = 0 the statistics of set
- * `set` ([rows][cols / 32] pairs of floats), 1 the vectors c then d (padded
- * to the pack's columns). Folds are numbered in kernel order. A diagnostic
- * with no counterpart in the reference (whose kernels run one per spec); the
- * fold itself changes no kernel's bindings or results beyond rounding. */
+ * LN(x) W + b = rstd ((x - mean) (gamma W)) + d with d = beta W + b, the
+ * writer of x leaving each row's 32-column block statistics (mean, sum of
+ * squared deviations) and the LayerNorm launching nothing. In f32 storage the
+ * writer also leaves x centred per block (x less its block's mean, the
+ * "shadow"), and the reader adds sum_b (mean_b - mean) cb[b] with cb[b] the
+ * column sums of gamma W over block b, so no product carries x's common
+ * offset; in f16 storage the reader computes x (gamma W) - mean c with c the
+ * column sums. bl_kernels_fold_read copies fold `fold`'s device buffers out
+ * after waiting for the stream: what = 0 the statistics of set `set`
+ * ([rows][cols / 32] pairs of floats), 1 the vectors c, d (each padded to the
+ * pack's columns n_pad) and cb ([n_pad][32]), 2 the shadow of set `set`
+ * (hi then lo bf16 planes for bf16x3 math, f32 for the f32 matrix cores).
+ * Folds are numbered in kernel order. A diagnostic with no counterpart in
+ * the reference (whose kernels run one per spec); the fold itself changes no
+ * kernel's bindings or results beyond rounding. */
 int bl_kernels_fold_read(bl_kernels *kernels, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes);
 /* The GPU kernel launches behind one bl_kernels_encode_range(first, count,
  * set) call, counted as the kernel nodes of the HIP graph that call replays

@@ -72,6 +72,39 @@ def test_the_benchmark_workload_vit_s_518_f32_matches_the_oracle_within_1e_4(ctx
     prep.close()
 
 
+@pytest.mark.parametrize("math", [hip.F32_MATH_SPLIT_BF16, hip.F32_MATH_MFMA_F32])
+def test_the_vit_s_518_workload_with_offset_rows_matches_the_oracle_within_1e_4(ctx, math):
+    """The benchmark's ViT-S/14 518 workload with 30 added to every position
+    embedding: every row of the residual stream then carries a common offset
+    about 30 times its spread, which the reference's LayerNorm removes before
+    anything multiplies it (crates/beatlm/src/codegen/wgsl.rs:519-585). All
+    24 LayerNorms are folded into their products; the 12-block output stays
+    within 1e-4 of the oracle in both f32 maths."""
+    ctx.set_f32_math(math)
+    try:
+        cfg = dict(bench.CONFIGS["vit-s-518"])
+        g, emb, block_ids, tokens = bench.build_encoder(cfg)
+        vals = bench.synthetic_values(cfg, emb, block_ids, tokens, np.float32, 2024)
+        vals[emb.pos] = (vals[emb.pos] + 30.0).astype(np.float32)
+        prep = ir.prepare(ctx, g, dtype=hip.F32)
+        labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+        assert sum("folded into" in s for s in labels) == 24, labels
+        for tid, v in vals.items():
+            prep.write(tid, v)
+        prep.run()
+        ctx.synchronize()
+        got = prep.read(block_ids[-1].output)
+        prep.close()
+    finally:
+        ctx.set_f32_math(hip.F32_MATH_SPLIT_BF16)
+    want = oracle_encoder(cfg, emb, block_ids, tokens, vals)
+    rows = want.astype(np.float64).reshape(tokens, cfg["width"])
+    err = max_abs_err(got, want)
+    print(f"vit-s-518 with offset rows (row mean {rows.mean(1).mean():.1f}, spread {rows.std(1).mean():.2f}), "
+          f"f32 math {math}: max abs error {err:.3e}")
+    assert err <= 1e-4, f"max abs error {err:.3e} above 1e-4"
+
+
 def test_the_vit_b_518_encoder_in_f16_is_within_2e_2_of_the_oracle(ctx):
     prep, cfg, emb, block_ids, tokens, vals = run_encoder(ctx, bench.CONFIGS["vit-b-518"])
     prep.run()

@@ -1,6 +1,8 @@
 """LayerNorms folded into the products that read them: LN(x) W + b computed
-as rstd (x (gamma W) - mean c) + d inside the product, with x's row
-statistics left by the product that wrote x. The fold must give the
+inside the product from x's row statistics, which the product that wrote x
+leaves: in f32 storage from x centred per 32-column block (the shadow) plus
+the block means' correction, in f16 storage as rstd (x (gamma W) - mean c)
++ d. The fold must give the
 LayerNorm-then-product result within the f32 bar (against the oracle's
 LayerNorm and matmul), whatever order the host encodes the kernels in:
 the LayerNorm or its reader encoded alone, x rewritten by the host in
@@ -115,6 +117,94 @@ def test_a_folded_layernorm_matches_the_layernorm_then_the_product(ctx, prepared
     np.testing.assert_allclose(vec[M:], v[B2] @ w1 + v[B1], atol=2e-5)
 
 
+def bf16_words(w: np.ndarray) -> np.ndarray:
+    """bf16 values (as uint16 words) widened to float64."""
+    return (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+def read_shadow(prep, math, t=T, d=D) -> np.ndarray:
+    """The fold's shadow as the consumer reads it: hi + lo of the bf16 planes
+    for bf16x3, the f32 values for the f32 matrix cores."""
+    raw = prep.kernels.fold_read(0, 2, t * d)
+    if math == hip.F32_MATH_SPLIT_BF16:
+        w = raw.view(np.uint16)
+        return bf16_words(w[: t * d]) + bf16_words(w[t * d:])
+    return raw.astype(np.float64)
+
+
+def centred(x, t=T, d=D) -> np.ndarray:
+    """x less each row's 32-column block means (float64)."""
+    b = x.astype(np.float64).reshape(t, d // 32, 32)
+    return (b - b.mean(2, keepdims=True)).reshape(-1)
+
+
+@pytest.mark.parametrize("math", [hip.F32_MATH_SPLIT_BF16, hip.F32_MATH_MFMA_F32])
+@pytest.mark.parametrize("offset", [10.0, 30.0, 100.0])
+def test_a_folded_layernorm_is_shift_invariant(ctx, prepared, math, offset):
+    """Rows whose mean is 10, 30 and 100 times their spread: x1 = x + ls (.)
+    (v Wo + bo) with x = offset + U(-1, 1). The reference normalises x - mean
+    before anything multiplies it, two passes, mean first
+    (crates/beatlm/src/codegen/wgsl.rs:519-585,
+    crates/beatlm-bench/src/reference.rs:247-270), so its result does not
+    depend on the offset; the fold must stay within the f32 bar (max abs
+    error <= 1e-4 against the oracle's LayerNorm and matmul) at every offset,
+    in both f32 maths. Its shadow holds x1 less each block's mean."""
+    prep = prepared(math)
+    v = values()
+    v[X] = (offset + v[X] / 2).astype(np.float32)
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    ctx.synchronize()
+    x1 = prep.read(X1)
+    spread = float(np.std(x1.astype(np.float64).reshape(T, D), axis=1).mean())
+    got = prep.read(OUT)
+    want = want_out(x1, v)
+    err = float(np.max(np.abs(got.astype(np.float64) - want)))
+    print(f"folded LayerNorm, rows at {offset} (mean / spread {offset / spread:.0f}), f32 math {math}: "
+          f"max abs error {err:.3e}")
+    assert_close(got, want, f"offset {offset}, f32 math {math}")
+    assert err <= 1e-4
+    # The shadow: x1 less its block means as the statistics hold them (the
+    # f32 difference), as the consumer multiplies it: bf16x3's hi + lo within
+    # 2^-16 of each value, the f32 matrix cores' exactly. The block means are
+    # within an f32 rounding of x1's.
+    st = prep.kernels.fold_read(0, 0, T * (D // 32) * 2).reshape(T, D // 32, 2)
+    np.testing.assert_allclose(st[:, :, 0], x1.astype(np.float64).reshape(T, D // 32, 32).mean(2),
+                               rtol=4e-7, atol=1e-6)
+    cx = (x1.reshape(T, D // 32, 32) - st[:, :, :1]).astype(np.float64).ravel()
+    sh = read_shadow(prep, math)
+    if math == hip.F32_MATH_SPLIT_BF16:
+        assert np.all(np.abs(sh - cx) <= 2.0 ** -16 * np.abs(cx)), float(np.max(np.abs(sh - cx)))
+    else:
+        assert np.array_equal(sh, cx)
+    assert float(np.max(np.abs(cx - centred(x1)))) <= 2e-5 * offset
+
+
+@pytest.mark.parametrize("math", [hip.F32_MATH_SPLIT_BF16, hip.F32_MATH_MFMA_F32])
+def test_a_folded_layernorm_with_an_outlier_channel(ctx, prepared, math):
+    """Every seventh row carries one channel 500 above the rest (a different
+    channel each time): the row's variance is dominated by it, and the
+    product after the fold stays within the f32 bar."""
+    prep = prepared(math)
+    v = values()
+    x = v[X].reshape(T, D).copy()
+    rows = np.arange(0, T, 7)
+    x[rows, (rows * 37) % D] += 500.0
+    v[X] = x.ravel()
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    ctx.synchronize()
+    x1 = prep.read(X1)
+    got = prep.read(OUT)
+    want = want_out(x1, v)
+    err = float(np.max(np.abs(got.astype(np.float64) - want)))
+    print(f"folded LayerNorm, outlier channels, f32 math {math}: max abs error {err:.3e}")
+    assert_close(got, want, f"outlier channels, f32 math {math}")
+    assert err <= 1e-4
+
+
 def test_a_folded_layernorm_in_f16_storage_is_within_the_f16_bar(ctx, prepared):
     prep = prepared(dtype=hip.F16)
     v = values(f16=True)
@@ -127,6 +217,26 @@ def test_a_folded_layernorm_in_f16_storage_is_within_the_f16_bar(ctx, prepared):
     got = prep.read(OUT).astype(np.float32)
     err = float(np.max(np.abs(got - want_out(x1, v32))))
     print(f"folded LayerNorm, f16 storage: max abs error {err:.3e}")
+    assert err <= 2e-2
+
+
+@pytest.mark.parametrize("offset", [10.0, 30.0])
+def test_a_folded_layernorm_in_f16_storage_with_offset_rows(ctx, prepared, offset):
+    """f16 storage keeps x uncentred (the product reads x itself and
+    subtracts mean c in f32): rows at 10 and 30 times their spread stay
+    within the f16 bar."""
+    prep = prepared(dtype=hip.F16)
+    v = values(f16=True)
+    v[X] = (offset + v[X].astype(np.float32) / 2).astype(np.float16)
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    ctx.synchronize()
+    x1 = prep.read(X1).astype(np.float32)
+    v32 = {k: a.astype(np.float32) for k, a in v.items()}
+    got = prep.read(OUT).astype(np.float32)
+    err = float(np.max(np.abs(got - want_out(x1, v32))))
+    print(f"folded LayerNorm, f16 storage, rows at {offset}: max abs error {err:.3e}")
     assert err <= 2e-2
 
 
