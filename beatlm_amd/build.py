@@ -73,12 +73,25 @@ def _compile(src: str) -> pathlib.Path:
     return out
 
 
-def build_library(jobs: int | None = None) -> pathlib.Path:
+def _stale(src: str) -> bool:
+    """Whether src's object is older than src or any header it may include."""
+    out = OBJ / (src + ".o")
+    if not out.exists():
+        return True
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), *CSRC.glob("*.inc"), *(REPO / "include").glob("*.h")]
+    return any(d.stat().st_mtime > out.stat().st_mtime for d in deps)
+
+
+def build_library(jobs: int | None = None, incremental: bool = False) -> pathlib.Path:
+    """Compiles every source (incremental: only those whose object is stale)
+    and links the library."""
     OBJ.mkdir(exist_ok=True)
     sources = [s for s in SOURCES if (CSRC / s).exists()]
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
+    todo = [s for s in sources if _stale(s)] if incremental else sources
+    jobs = jobs or min(max(1, len(todo)), max(1, (os.cpu_count() or 2)))
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
-        objects = list(pool.map(_compile, sources))
+        list(pool.map(_compile, todo))
+    objects = [OBJ / (s + ".o") for s in sources]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -101,5 +114,9 @@ def build() -> None:
 
 
 if __name__ == "__main__":
-    build()
+    if "--incremental" in sys.argv:
+        build_oracle()
+        build_library(incremental=True)
+    else:
+        build()
     print(LIB)

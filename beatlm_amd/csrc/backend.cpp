@@ -1409,6 +1409,9 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 L.family = Family::FLASH;
                 const uint32_t t_pad = (d[0] + 63) / 64 * 64;
                 const FlashPlan fp = plan_flash(fmath, d[0], d[1], pt.start, pt.end, ctx->compute_units);
+                if (!fp.fits)
+                    return bad(BL_ERR_TOO_LARGE, "kernel %s: %u tokens x %u heads is beyond the flash kernel's run arithmetic",
+                               name.c_str(), d[0], d[1]);
                 L.fl = FlashArgs{};
                 L.fl.qkv = rd(0);
                 L.fl.out = out_ptr;

@@ -212,7 +212,8 @@ template <> __device__ __forceinline__ float representable<Math::F16>(float v) {
 template <> __device__ __forceinline__ float representable<Math::SPLIT>(float v) { return (float)(__bf16)v; }
 
 // The run of units [begin, end) of virtual workgroup v out of G: equal
-// contiguous shares of U. The planner keeps U * G below 2^32.
+// contiguous shares of U. The planner refuses shapes with U * G of 2^32 or
+// more (FlashPlan::fits).
 __host__ __device__ inline uint32_t run_begin(uint32_t v, uint32_t U, uint32_t G) { return v * U / G; }
 // The virtual workgroup whose run holds unit u.
 __host__ __device__ inline uint32_t run_of(uint32_t u, uint32_t U, uint32_t G) { return ((u + 1) * G - 1) / U; }
@@ -906,7 +907,21 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
         // One workgroup per CU, the same number on each XCD (its 8 waves are
         // two per SIMD); the pairs and their units are shared out per XCD.
         p.wgs = std::max<uint32_t>(8, compute_units / 8 * 8);
-        const uint32_t pairs = heads * p.qtiles;
+        // The run arithmetic is 32-bit: (pairs + 1) * 8, and each XCD's
+        // units times its runs, stay below 2^32.
+        const uint64_t pairs64 = (uint64_t)heads * p.qtiles;
+        if ((pairs64 + 1) * 8 >= (1ull << 32)) {
+            p.fits = false;
+            return p;
+        }
+        const uint32_t pairs = (uint32_t)pairs64;
+        for (uint32_t x = 0; x < 8; x++) {
+            const uint64_t n = run_begin(x + 1, pairs, 8) - run_begin(x, pairs, 8);
+            if ((n * kt + 1) * (p.wgs / 8) >= (1ull << 32)) {
+                p.fits = false;
+                return p;
+            }
+        }
         for (uint32_t item = 0; item < pairs && !p.merge; item++) {
             const uint32_t x = run_of(item, pairs, 8);
             const XcdShare sh = xcd_share(pairs, kt, p.wgs, x);
@@ -918,6 +933,27 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
     }
     p.scratch_bytes = operand_bytes(m, heads, t_pad) + extra;
     return p;
+}
+
+int flash_plan_check(uint32_t tokens, uint32_t heads, uint32_t compute_units, bool f16, uint64_t *units) {
+    const FlashPlan p = plan_flash(f16 ? Math::F16 : Math::SPLIT, tokens, heads, 0, tokens, compute_units);
+    if (!p.fits) return BL_ERR_TOO_LARGE;
+    const uint32_t kt = (tokens + KT - 1) / KT, pairs = heads * p.qtiles;
+    uint64_t total = 0;
+    for (uint32_t x = 0; x < 8; x++) {
+        const XcdShare sh = xcd_share(pairs, kt, p.wgs, x);
+        total += sh.U;
+        if (sh.U == 0) continue;
+        if (sh.G == 0 || sh.G > p.wgs / 8 || run_begin(0, sh.U, sh.G) != 0 || run_begin(sh.G, sh.U, sh.G) != sh.U)
+            return BL_ERR_KERNEL;
+        for (uint32_t v = 0; v < sh.G; v++) {
+            const uint32_t b = run_begin(v, sh.U, sh.G), e = run_begin(v + 1, sh.U, sh.G);
+            if (e < b) return BL_ERR_KERNEL;
+            if (e > b && (run_of(b, sh.U, sh.G) != v || run_of(e - 1, sh.U, sh.G) != v)) return BL_ERR_KERNEL;
+        }
+    }
+    if (units) *units = total;
+    return total == p.units ? BL_OK : BL_ERR_KERNEL;
 }
 
 void bind_flash_scratch(FlashArgs &a, Math m, void *base) {
@@ -935,3 +971,11 @@ void bind_flash_scratch(FlashArgs &a, Math m, void *base) {
 }
 
 }  // namespace bl
+
+// Test hook (no GPU work): flash_plan_check for a shape.
+extern "C" int bl_flash_plan_check(uint32_t tokens, uint32_t heads, uint32_t compute_units, uint32_t dtype,
+                                   uint64_t *units) {
+    if (tokens == 0 || heads == 0 || compute_units == 0 || (dtype != BL_F32 && dtype != BL_F16))
+        return BL_ERR_INVALID_ARGUMENT;
+    return bl::flash_plan_check(tokens, heads, compute_units, dtype == BL_F16, units);
+}

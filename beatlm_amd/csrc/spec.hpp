@@ -186,7 +186,17 @@ struct FlashPlan {
     uint32_t splits = 1, qtiles = 0, wgs = 0, merge = 0;
     uint64_t units = 0;
     uint64_t scratch_bytes = 0;
+    // False when the shape's unit runs would overflow the kernels' 32-bit
+    // run arithmetic (units of one XCD times its runs, 2^32 or more): the
+    // backend refuses such a kernel.
+    bool fits = true;
 };
+// Host check of plan_flash's unit runs for a shape (f16 and bf16x3 math):
+// every XCD's units [0, U) are covered by its G runs in order, each unit by
+// exactly one (run_begin monotone from 0 to U, run_of agreeing at every
+// run's ends). BL_OK, BL_ERR_TOO_LARGE when the plan refuses the shape, or
+// BL_ERR_KERNEL when the runs are wrong.
+int flash_plan_check(uint32_t tokens, uint32_t heads, uint32_t compute_units, bool f16, uint64_t *units);
 
 // The DPT head's gathers: each output element from a few input values.
 enum class Dpt : int { CONV_TRANSPOSE = 0, RESIZE = 1 };

@@ -13,7 +13,9 @@
 // In host code `scratch` names a host-side stand-in, not a device address:
 // the array's address on a device comes from hipGetSymbolAddress, called
 // once per device (with that device current) on the entry point's first call
-// there, and only that address is handed to kernels.
+// there (kept once found; a failed lookup is tried again on the next call),
+// and only that address is handed to kernels. The call makes the context's
+// device current and restores the caller's current device before returning.
 //
 // Every call on a GPU shares that GPU's array: calls that overlap on one GPU
 // (two streams, two contexts) race. Nothing in the array needs to start at
@@ -34,19 +36,35 @@ static __device__ __align__(256) char scratch[BL_STATIC_SCRATCH_BYTES];
 
 constexpr int MAX_DEVICES = 64;
 void *device_scratch[MAX_DEVICES];
-hipError_t device_status[MAX_DEVICES];
-std::once_flag device_once[MAX_DEVICES];
+std::mutex device_mutex;
 
-// The array's address on `device` (current), looked up once.
+// The array's address on `device` (current): looked up on the first call
+// there and kept once found; a failed lookup is tried again next call.
 hipError_t scratch_on(int device, void **out) {
-    std::call_once(device_once[device], [device] {
+    std::lock_guard<std::mutex> lock(device_mutex);
+    if (!device_scratch[device]) {
         void *p = nullptr;
-        device_status[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        device_scratch[device] = device_status[device] == hipSuccess ? p : nullptr;
-    });
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        device_scratch[device] = p;
+    }
     *out = device_scratch[device];
-    return device_status[device];
+    return hipSuccess;
 }
+
+// Makes `device` current for the call and restores the caller's device after.
+struct DeviceScope {
+    int prev = -1;
+    hipError_t status = hipSuccess;
+    explicit DeviceScope(int device) {
+        status = hipGetDevice(&prev);
+        if (status == hipSuccess && prev != device) status = hipSetDevice(device);
+        else if (status == hipSuccess) prev = -1;  // already current: nothing to restore
+    }
+    ~DeviceScope() {
+        if (prev >= 0) hipSetDevice(prev);
+    }
+};
 
 int fail(bl_ctx *ctx, int code, const char *fmt, unsigned long long a, unsigned long long b) {
     char msg[256];
@@ -69,11 +87,15 @@ extern "C" int bl_flash_attention_static(bl_ctx *ctx, const void *qkv, void *out
     const bl::Math m = dtype == BL_F16 ? bl::Math::F16
                      : bl_f32_math_of(ctx) == BL_F32_MATH_MFMA_F32 ? bl::Math::F32 : bl::Math::SPLIT;
     const bl::FlashPlan plan = bl::plan_flash(m, tokens, heads, 0, tokens, bl_compute_units_of(ctx));
+    if (!plan.fits)
+        return fail(ctx, BL_ERR_TOO_LARGE, "flash attention (static): %llu tokens x %llu heads is beyond the kernel's run arithmetic",
+                    (unsigned long long)tokens, (unsigned long long)heads);
     if (plan.scratch_bytes > BL_STATIC_SCRATCH_BYTES)
         return fail(ctx, BL_ERR_TOO_LARGE,
                     "flash attention (static): this shape needs %llu bytes of scratch, the static array holds %llu",
                     (unsigned long long)plan.scratch_bytes, (unsigned long long)BL_STATIC_SCRATCH_BYTES);
-    hipError_t e = hipSetDevice(device);
+    const DeviceScope scope(device);
+    hipError_t e = scope.status;
     void *base = nullptr;
     if (e == hipSuccess) e = scratch_on(device, &base);
     if (e != hipSuccess || !base) return bl_fail(ctx, BL_ERR_HIP, "flash attention (static): no address for the scratch array");

@@ -217,6 +217,7 @@ _SIGNATURES = {
     "bl_kernels_range_launches": (C.c_int, [_VP, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint32)]),
     "bl_spin": (C.c_int, [_VP, C.c_uint32]),
     "bl_flash_attention_static": (C.c_int, [_VP, _VP, _VP, C.c_uint32, C.c_uint32, C.c_float, C.c_uint32]),
+    "bl_flash_plan_check": (C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]),
 }
 
 _lib = None

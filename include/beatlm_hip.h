@@ -362,11 +362,22 @@ int bl_kernels_range_launches(bl_kernels *kernels, uint32_t first, uint32_t coun
  * each GPU it has run this on until the process ends; a shape needing more
  * is refused with BL_ERR_TOO_LARGE and a message. Nothing is allocated, the
  * first call on a device aside, which looks the array's address up (and so
- * loads the code object holding it). Every call on a GPU shares that GPU's
- * array: calls that overlap on one GPU race. */
+ * loads the code object holding it; a failed lookup is tried again on the
+ * next call). The call makes the context's device current and restores the
+ * caller's current device before it returns. Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU race. */
 #define BL_STATIC_SCRATCH_BYTES (64ull << 20)
 int bl_flash_attention_static(bl_ctx *ctx, const void *qkv, void *out, uint32_t tokens,
                               uint32_t heads, float scale, uint32_t dtype);
+
+/* Diagnostic (no GPU work, no context): checks the flash kernel's plan for
+ * tokens x heads on compute_units CUs (dtype BL_F32 with bf16x3 math, or
+ * BL_F16): the (head, query tile, key tile) units of each XCD are covered by
+ * its runs of workgroups in order, each unit by exactly one run. BL_OK with
+ * *units the units planned, BL_ERR_TOO_LARGE when the shape is beyond the
+ * kernel's 32-bit run arithmetic (kernels for it are refused the same way),
+ * BL_ERR_KERNEL when the runs are wrong. No counterpart in the reference. */
+int bl_flash_plan_check(uint32_t tokens, uint32_t heads, uint32_t compute_units, uint32_t dtype, uint64_t *units);
 
 /* ---- slice timer: hipEvent pairs per slice, a ring of frames ---- */
 #define BL_TIMER_RING_DEPTH 3

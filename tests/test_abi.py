@@ -91,3 +91,29 @@ def test_without_a_device_a_context_is_an_error_not_a_crash():
         pytest.skip("a GPU is visible")
     assert rc in (hip.ERR_HIP, hip.ERR_INVALID_ARGUMENT)
     assert lib.bl_ctx_create(-1, C.byref(h)) != hip.OK
+
+
+@pytest.mark.parametrize("tokens,heads", [(1, 1), (17, 2), (257, 6), (1370, 6), (1370, 12), (1370, 16), (5477, 6),
+                                          (65_536, 16), (1_000_000, 16), (3_000_000, 32)])
+@pytest.mark.parametrize("dtype", [hip.F32, hip.F16])
+def test_the_flash_plan_covers_every_unit_once(tokens, heads, dtype):
+    """The flash kernel's (head, 256-query tile, 64-key tile) units, dealt in
+    contiguous runs per XCD, are each covered by exactly one run, up to the
+    longest sequences its 32-bit run arithmetic allows; beyond that the
+    plan refuses the shape rather than overflow."""
+    lib = hip.lib()
+    units = C.c_uint64()
+    rc = lib.bl_flash_plan_check(tokens, heads, 256, dtype, C.byref(units))
+    want = heads * -(-tokens // 256) * -(-tokens // 64)
+    if rc == hip.ERR_TOO_LARGE:
+        assert want * 32 >= 2**32, (tokens, heads, want)
+        return
+    assert rc == hip.OK, rc
+    assert units.value == want
+
+
+def test_the_flash_plan_refuses_shapes_beyond_its_run_arithmetic():
+    lib = hip.lib()
+    units = C.c_uint64()
+    assert lib.bl_flash_plan_check(2_000_000_000, 16, 256, hip.F16, C.byref(units)) == hip.ERR_TOO_LARGE
+    assert lib.bl_flash_plan_check(0, 16, 256, hip.F16, C.byref(units)) == hip.ERR_INVALID_ARGUMENT

@@ -9,6 +9,7 @@ storage with f32 accumulation.
   :520-544; the reference's own encoder test, crates/beatlm-bench/src/vit.rs
   :240-309, runs one such block).
 - ViT-B/14 at 518 pixels: 12 f16 blocks of 1370 tokens, width 768.
+- ViT-S/14 at 1036 pixels (5477 tokens, f16): the first two blocks.
 - ViT-L/14 at 518 pixels, four frames: four job slots of one program, each
   slot one binding set that rebinds the image and the output
   (crates/beatlm/src/codegen/kernels.rs:120-170, crates/beatlm-host/src/
@@ -115,6 +116,23 @@ def test_the_vit_b_518_encoder_in_f16_is_within_2e_2_of_the_oracle(ctx):
     print(f"vit-b-518, 12 f16 blocks, 1370 tokens x 768: max abs error {err:.3e} (|want| max {np.abs(want).max():.2f})")
     assert err <= 2e-2, f"max abs error {err:.3e} above 2e-2"
     prep.close()
+
+
+def test_two_vit_s_1036_blocks_in_f16_are_within_2e_2_of_the_oracle(ctx):
+    """Config 5's encoder (5477 tokens, f16) through its first two blocks,
+    with the patch embedding, class token and positions, against the
+    oracle's composition; its full 12-block depth is checked split against
+    unsplit by the frame loop's test."""
+    prep, cfg, emb, block_ids, tokens, vals = run_encoder(ctx, bench.CONFIGS["vit-s-1036"], blocks=2)
+    assert tokens == 5477
+    prep.run()
+    ctx.synchronize()
+    got = prep.read(block_ids[-1].output).astype(np.float32)
+    prep.close()
+    want = oracle_encoder(cfg, emb, block_ids, tokens, vals)
+    err = max_abs_err(got, want)
+    print(f"vit-s-1036, 2 f16 blocks, 5477 tokens: max abs error {err:.3e} (|want| max {np.abs(want).max():.2f})")
+    assert err <= 2e-2, f"max abs error {err:.3e} above 2e-2"
 
 
 def frame_images(cfg, frames):
