@@ -1263,22 +1263,35 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 // k-steps, so that every staged row is whole 128-byte lines: a
                 // wave's load touching 16 half lines reads a third as fast as
                 // one touching 8 whole lines (15 against 48 bytes per clock per
-                // CU from L2, measured). Two-stage rings, so that 2 to 3
-                // workgroups fit a CU (three for the longest k in f16). The
-                // tiles follow the rounds of workgroups the chip runs: bf16x3
-                // takes 64 x 64 for wide outputs whose tiles fit one round at
-                // two per CU (QKV: 11.4 -> 9.1 us), else 32 x 64 (fc1 17.9 ->
-                // 14.5); f16 takes 64 x 64, or 32 x 64 for square projections
-                // of few rows (ViT-L's QKV 38.4 -> 24.1 us, fc1 54.4 -> 33.0).
-                // With fewer 32 x 64 tiles than CUs (small images) the deeper
-                // rings of 32-wide steps hide more latency and stay.
+                // CU from L2, measured). Two-stage rings in bf16x3, so that 2
+                // to 3 workgroups fit a CU. The tiles follow the rounds of
+                // workgroups the chip runs: bf16x3 takes 64 x 64 for wide
+                // outputs whose tiles fit one round at two per CU (QKV: 11.4
+                // -> 9.1 us), else 32 x 64 (fc1 17.9 -> 14.5); f16 takes 64 x
+                // 64, or 32 x 64 for square projections of few rows (ViT-L's
+                // QKV 38.4 -> 24.1 us, fc1 54.4 -> 33.0). An f16 product's
+                // tiles wait on L2 latency rather than bandwidth, so its ring
+                // deepens with the k-steps it has to hide it over: 2 stages
+                // below 12 steps, 3 below 24, else 4 (ViT-L at 518: QKV 25.9
+                // -> 24.5 us, fc2 30.1 -> 27.3; ViT-B: fc2 22.4 -> 21.0; ViT-S
+                // at 1036: fc2 26.2 -> 21.8). Its square projections of few
+                // rows keep 2 (ViT-L's out-projection: 9.5 against 10.8 with
+                // 3), and so do grids of more than 5 tiles per CU (ViT-L's fc1,
+                // 1408 tiles: 30.4 us against 32.9 to 34.0 with 3). With fewer
+                // 32 x 64 tiles than CUs (small images) the deeper rings of
+                // 32-wide steps hide more latency and stay.
                 uint32_t kslices = 1;
                 if ((fmath == Math::F16 || fmath == Math::SPLIT) && !patch && !conv && gk % 64 == 0 &&
                     wgs_of(TILE_32x64) >= ctx->compute_units) {
                     kslices = 2;
                     ga.kgroups = 1;
-                    ga.stages = fmath == Math::F16 && gk >= 2048 ? 3 : 2;
-                    if (fmath == Math::F16) chosen = (gn <= 1024 && gk <= 1024 && rows <= 2048) ? TILE_32x64 : TILE_64x64;
+                    ga.stages = 2;
+                    if (fmath == Math::F16) {
+                        const bool square_few = gn <= 1024 && gk <= 1024 && rows <= 2048;
+                        chosen = square_few ? TILE_32x64 : TILE_64x64;
+                        if (!square_few)
+                            ga.stages = gk / 64 >= 24 ? 4 : gk / 64 >= 12 && wgs_of(TILE_64x64) <= 5ull * ctx->compute_units ? 3 : 2;
+                    }
                     else chosen = (gn >= 1024 && w64 <= 2ull * ctx->compute_units) ? TILE_64x64 : TILE_32x64;
                     // bf16x3 outputs of whole 96-column tiles, at least 1536
                     // wide, that fit one round at two 64 x 96 workgroups per CU
