@@ -62,9 +62,11 @@ int hip_fail(bl_ctx *ctx, hipError_t e, const char *what) {
 constexpr uint32_t PLACEMENT_ALIGNMENT = 256;
 
 // Whether the process runs under rocprofv3, which sets these for the program
-// it starts. HIP-graph capture and replay is not used there: a host
-// segmentation fault was recorded under rocprofv3 while the depth model's
-// programs were captured, whose cause was not established.
+// it starts. HIP-graph capture and replay is not used there, so that profiled
+// runs are not the ones that ended in a host segmentation fault under
+// rocprofv3 with the depth model's programs captured. A second such fault
+// came with graphs off, on a thread this library never runs on, so capture is
+// not known to be the cause; that case is simply not repeated.
 bool profiler_attached() {
     static const bool attached = [] {
         const bool on = getenv("ROCPROF_OUTPUT_PATH") || getenv("ROCPROFILER_LIBRARY_CTOR");
