@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -601,16 +602,21 @@ struct bl_kernels {
     bl_arenas *arenas = nullptr;
     std::vector<Kernel> kernels;
     uint32_t sets = 1;
-    char *workspace = nullptr;  // the one allocation holding the three below
+    // The one allocation holding the packed weights, the attention scratch,
+    // the split-k partial sums and the folds' buffers, placed by lifetime.
+    char *workspace = nullptr;
     uint64_t workspace_bytes = 0;
     void *scratch = nullptr;
-    float *partials = nullptr;  // split-k GEMMs' partial sums, shared as the attention scratch is
     std::vector<Pack> packs;
     void *pack_buffer = nullptr;
     uint64_t packs_made = 0;
     KvState kv;
     std::vector<Fold> folds;
     FoldState fold_state;  // [fold * sets + set]
+    // Fold entries ([fold * sets + set]) whose workspace bytes another entry
+    // shares (their lifetimes are disjoint), and per kernel the entries its
+    // split-k partial sums overwrite: writing one makes the others stale.
+    std::vector<std::vector<uint32_t>> fold_alias, kernel_clobbers;
     std::vector<RangeGraph> graphs;
     // Graphs replay fixed launches: not used when a kernel of the program
     // rewrites a packed weight's source (the pack must rerun in between),
@@ -1009,6 +1015,55 @@ extern "C" int bl_kernels_create(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *
     return bl_kernels_create_internal(ctx, arenas, specs, n, sets, n_sets, nullptr, 0, out);
 }
 
+namespace {
+
+// One item of the backend's workspace: its bytes, the kernels from its first
+// writer to its last reader (inclusive), its binding set (-1: any), and its
+// offset once placed.
+struct WsItem {
+    uint64_t size;
+    uint32_t first, last;
+    int set;
+    uint64_t at;
+};
+
+// Places the items as the memory plan places tensors in an arena
+// (memory.rs:285-338): by size, descending (ties in item order), each at the
+// lowest 256-byte aligned offset clear of every placed item it may be live
+// with. Items of two different binding sets are taken to be live together
+// (a frame loop may interleave the sets' ranges); otherwise two items are
+// live together when their kernel intervals overlap. Returns the bytes the
+// placement spans.
+uint64_t place_workspace(std::vector<WsItem> &items) {
+    std::vector<size_t> order(items.size());
+    for (size_t i = 0; i < order.size(); i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](size_t a, size_t b) { return items[a].size > items[b].size; });
+    auto together = [&](const WsItem &a, const WsItem &b) {
+        if (a.set >= 0 && b.set >= 0 && a.set != b.set) return true;
+        return a.first <= b.last && b.first <= a.last;
+    };
+    std::vector<size_t> placed;
+    uint64_t total = 0;
+    for (size_t i : order) {
+        WsItem &it = items[i];
+        std::vector<std::pair<uint64_t, uint64_t>> busy;
+        for (size_t j : placed)
+            if (together(it, items[j])) busy.push_back({items[j].at, items[j].at + items[j].size});
+        std::sort(busy.begin(), busy.end());
+        uint64_t at = 0;
+        for (auto [lo, hi] : busy) {
+            if (at + it.size <= lo) break;
+            at = std::max(at, (hi + 255) / 256 * 256);
+        }
+        it.at = at;
+        total = std::max(total, at + it.size);
+        placed.push_back(i);
+    }
+    return total;
+}
+
+}  // namespace
+
 extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const bl_spec *specs, uint32_t n,
                                           const bl_binding_set *sets, uint32_t n_sets, const uint32_t *internal,
                                           uint32_t n_internal, bl_kernels **out) {
@@ -1027,7 +1082,6 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     ks->sets = n_sets;
     uint64_t scratch_bytes = 0;
     std::vector<std::pair<size_t, size_t>> flash_users;  // (kernel, set) whose FlashArgs need scratch
-    uint64_t partial_bytes = 0;
     std::vector<std::pair<size_t, size_t>> split_users;  // (kernel, set) of split-k GEMMs
 
     auto bad = [&](int code, const char *fmt, auto... args) {
@@ -1348,10 +1402,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 // (Split k for plain products with few tiles measured slower: the
                 // reduce launch and the partial sums cost more than the shorter
                 // k-loops save, 1.00 -> 1.07 ms for the model at 182 pixels.)
-                if (ga.ksplit > 1) {
-                    partial_bytes = std::max<uint64_t>(partial_bytes, (uint64_t)ga.ksplit * rows * gn * sizeof(float));
-                    split_users.push_back({ki, si});
-                }
+                if (ga.ksplit > 1) split_users.push_back({ki, si});
                 L.gemm = ga;
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
@@ -1459,9 +1510,10 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     plan_prepends(ks, specs, n, internal, n_internal);
     plan_folds(ks, specs, n, sets, n_sets, internal, n_internal);
     // The backend's own device memory, one allocation beside the plan's
-    // arenas: the packed weights, then the split-k GEMMs' partial sums, then
-    // the attention scratch, then the folded LayerNorms' statistics and
-    // planes, each 256-byte aligned.
+    // arenas, laid out by lifetime (place_workspace): the packed weights and
+    // the attention scratch for the whole program, each split-k GEMM's
+    // partial sums for its own launch, each folded LayerNorm's statistics and
+    // planes from its producer to its consumer.
     auto align256 = [](uint64_t b) { return (b + 255) / 256 * 256; };
     for (const Kernel &k : ks->kernels)
         for (const Launch &L : k.per_set)
@@ -1483,34 +1535,64 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     }
     for (const Pack &pk : ks->packs)
         if (pk.used && pk.dynamic) ks->graphs_ok = false;
-    const uint64_t partial_at = pack_total, scratch_at = partial_at + align256(partial_bytes);
-    const uint64_t folds_at = scratch_at + align256(scratch_bytes);
-    uint64_t fold_bytes = 0;
+    std::vector<WsItem> items;
+    const uint32_t whole = n ? n - 1 : 0;
+    const size_t pack_item = items.size();
+    if (pack_total) items.push_back({pack_total, 0, whole, -1, 0});
+    const size_t scratch_item = items.size();
+    if (scratch_bytes) items.push_back({align256(scratch_bytes), 0, whole, -1, 0});
+    // Each split-k GEMM's partial sums: the largest over its binding sets,
+    // written and read within its own launch.
+    std::map<size_t, size_t> partial_item;  // kernel -> item
+    for (auto [ki, si] : split_users) {
+        const GemmArgs &ga = ks->kernels[ki].per_set[si].gemm;
+        const uint64_t b = align256((uint64_t)ga.ksplit * (ga.row1 - ga.row0) * ga.n * sizeof(float));
+        auto it = partial_item.find(ki);
+        if (it == partial_item.end()) {
+            partial_item[ki] = items.size();
+            items.push_back({b, (uint32_t)ki, (uint32_t)ki, -1, 0});
+        } else {
+            items[it->second].size = std::max(items[it->second].size, b);
+        }
+    }
+    const size_t fold_item = items.size();
     for (const Fold &f : ks->folds)
-        fold_bytes += ks->sets * (align256(fold_stats_bytes(f)) +
-                                  align256(fold_plane_bytes(f, ks->kernels[f.consumer].per_set[0])));
-    const uint64_t workspace = folds_at + fold_bytes;
+        for (uint32_t si = 0; si < ks->sets; si++)
+            items.push_back({align256(fold_stats_bytes(f)) + align256(fold_plane_bytes(f, ks->kernels[f.consumer].per_set[si])),
+                             f.producer, f.consumer, (int)si, 0});
+    const uint64_t workspace = place_workspace(items);
     if (workspace) {
         ks->workspace = (char *)bl_device_alloc(ctx, workspace);
         if (!ks->workspace)
-            return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of workspace (packed weights, partial sums, attention scratch)",
+            return bad(BL_ERR_HIP, "hipMalloc of %llu bytes of workspace (packed weights, partial sums, attention scratch, folds)",
                        (unsigned long long)workspace);
         ks->workspace_bytes = workspace;
     }
     if (pack_total) {
-        ks->pack_buffer = ks->workspace;
+        ks->pack_buffer = ks->workspace + items[pack_item].at;
         for (Kernel &k : ks->kernels)
             for (Launch &L : k.per_set)
                 if (L.pack >= 0) L.gemm.b = (char *)ks->pack_buffer + ks->packs[L.pack].dst_offset;
     }
-    if (partial_bytes) {
-        // Split-k GEMMs run one after another on the stream: one buffer serves
-        // them all, every element written by its split before the reduce reads it.
-        ks->partials = (float *)(ks->workspace + partial_at);
-        for (auto [ki, si] : split_users) ks->kernels[ki].per_set[si].gemm.partials = ks->partials;
+    // A split-k GEMM's partial sums, every element written by its split
+    // before the reduce reads it, share bytes with folds of disjoint
+    // lifetimes: its launch makes their statistics stale.
+    ks->kernel_clobbers.assign(n, {});
+    ks->fold_alias.assign(ks->folds.size() * ks->sets, {});
+    auto overlap = [&](size_t a, size_t b) {
+        return items[a].at < items[b].at + items[b].size && items[b].at < items[a].at + items[a].size;
+    };
+    for (auto [ki, item] : partial_item) {
+        for (auto [kj, sj] : split_users)
+            if (kj == ki) ks->kernels[kj].per_set[sj].gemm.partials = (float *)(ks->workspace + items[item].at);
+        for (size_t e = 0; e < ks->fold_alias.size(); e++)
+            if (overlap(item, fold_item + e)) ks->kernel_clobbers[ki].push_back((uint32_t)e);
     }
+    for (size_t e = 0; e < ks->fold_alias.size(); e++)
+        for (size_t g = 0; g < ks->fold_alias.size(); g++)
+            if (g != e && overlap(fold_item + e, fold_item + g)) ks->fold_alias[e].push_back((uint32_t)g);
     if (scratch_bytes) {
-        ks->scratch = ks->workspace + scratch_at;
+        ks->scratch = ks->workspace + items[scratch_item].at;
         // Kernels run one after another on the stream, so every flash kernel
         // uses the same scratch: operands, then partial outputs and statistics.
         for (auto [ki, si] : flash_users)
@@ -1554,17 +1636,16 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     }
     if (n_internal && !getenv("BL_NO_SPLIT_ACTIVATIONS")) keep_split_activations(ks, specs, n, internal, n_internal);
     if (!ks->folds.empty()) {
-        uint64_t at = folds_at;
-        for (Fold &f : ks->folds)
+        for (size_t fi = 0; fi < ks->folds.size(); fi++)
             for (uint32_t si = 0; si < ks->sets; si++) {
+                Fold &f = ks->folds[fi];
+                const uint64_t at = items[fold_item + fi * ks->sets + si].at;
                 LnStatsArgs &sa = f.stats[si];
                 sa.stats = (float *)(ks->workspace + at);
-                at += align256(fold_stats_bytes(f));
                 const Launch &G = ks->kernels[f.consumer].per_set[si];
                 const uint64_t planes = fold_plane_bytes(f, G);
-                sa.shadow = planes ? ks->workspace + at : nullptr;
+                sa.shadow = planes ? ks->workspace + at + align256(fold_stats_bytes(f)) : nullptr;
                 sa.planes = planes && G.math == Math::SPLIT ? (uint64_t)sa.rows * sa.cols : 0;
-                at += align256(planes);
             }
         apply_folds(ks);
     }
@@ -1704,6 +1785,13 @@ static Launch with_kv(const Launch &L, uint32_t i, KvState &kv) {
     return run;
 }
 
+static void stale(FoldState &fs, const std::vector<uint32_t> &entries) {
+    for (uint32_t e : entries) {
+        fs.valid[e] = 0;
+        fs.touched[e] = 1;
+    }
+}
+
 // Kernel i of binding set `set` as the attention scratch (kv) and the folded
 // LayerNorms' statistics (fs) require it, and their state after it: a folded
 // LayerNorm, or its consumer, whose statistics do not describe x as it now is
@@ -1720,6 +1808,7 @@ static hipError_t run_one(bl_kernels *k, uint32_t i, uint32_t set, hipStream_t s
             if (e != hipSuccess) return e;
             fs.valid[at] = 1;
             fs.touched[at] = 1;
+            stale(fs, k->fold_alias[at]);
         }
         if (L.fold_role == FOLD_LAYER_NORM) return hipSuccess;
     }
@@ -1734,6 +1823,10 @@ static hipError_t run_one(bl_kernels *k, uint32_t i, uint32_t set, hipStream_t s
             fs.touched[at] = 1;
         }
     }
+    // The producer's statistics and the split-k partial sums overwrite the
+    // folds that share their bytes.
+    if (L.fold >= 0 && L.fold_role == FOLD_PRODUCER) stale(fs, k->fold_alias[(size_t)L.fold * sets + set]);
+    stale(fs, k->kernel_clobbers[i]);
     return hipSuccess;
 }
 

@@ -319,7 +319,9 @@ int bl_kernels_time(bl_kernels *kernels, uint32_t kernel, uint32_t set, uint32_t
 uint64_t bl_kernels_packs_made(const bl_kernels *kernels);
 /* Bytes of device memory the kernels hold beside the plan's arenas, in one
  * allocation made by bl_kernels_create (0: none): packed weights, split-k
- * partial sums, attention scratch. No counterpart in the reference, whose
+ * partial sums, attention scratch, the folded LayerNorms' statistics and
+ * planes, placed by lifetime as the plan places tensors in an arena (items of
+ * disjoint kernel spans share bytes). No counterpart in the reference, whose
  * kernels hold no memory of their own; with the arenas' one allocation, a
  * program's device memory is these two allocations. */
 uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
@@ -337,7 +339,9 @@ uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
  * ([rows][cols / 32] pairs of floats), 1 the vectors c, d (each padded to the
  * pack's columns n_pad) and cb ([n_pad][32]), 2 the shadow of set `set`
  * (hi then lo bf16 planes for bf16x3 math, f32 for the f32 matrix cores).
- * Folds are numbered in kernel order. A diagnostic with no counterpart in
+ * Folds are numbered in kernel order. Folds whose producer-to-consumer spans
+ * do not overlap share bytes, so a fold's buffers hold what the last writer
+ * of those bytes left. A diagnostic with no counterpart in
  * the reference (whose kernels run one per spec); the fold itself changes no
  * kernel's bindings or results beyond rounding. */
 int bl_kernels_fold_read(bl_kernels *kernels, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes);
