@@ -13,6 +13,11 @@ Prints ONE JSON line. Everything is timed with inputs resident in HBM.
   python bench.py [--steps K] [--warmup W] [--config vit-s-518|vit-s-224|vit-b-518|vit-l-518x4|vit-s-1036]
                   [--f32-math split|mfma] [--no-cpu-baseline] [--frame-loop-frames N]
 
+For an f32 workload timed with bf16x3 math (the default), the line also
+carries `f32_mfma`: the same workload with the f32 matrix cores
+(v_mfma_f32_16x16x4_f32), its µs/block, per-kernel times and dominant group
+against their 157.3 TFLOP/s peak (--no-f32-mfma-line skips it).
+
 The same line carries `frame_loop`: the high-resolution encoder (ViT-S/14 at
 1036 x 1036, 5477 tokens, 12 blocks, f16) run as frame-budget slices at 60
 frames per second beside a render load spinning the GPU for 8 ms a frame,
@@ -782,6 +787,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="vit-s-518", choices=sorted(CONFIGS))
     ap.add_argument("--f32-math", default="split", choices=["split", "mfma"])
+    ap.add_argument("--no-f32-mfma-line", dest="f32_mfma_line", action="store_false",
+                    help="skip timing an f32 workload on the f32 matrix cores beside its bf16x3 line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip comparing the timed output with the oracle")
     ap.add_argument("--kernel-repeats", type=int, default=20)
@@ -908,6 +915,24 @@ def main() -> int:
         result["attention_tflops"] = attn["achieved"]
         result["attention_frac_of_mfma_peak"] = attn["frac"]
 
+    # An f32 workload with bf16x3 math: the same workload on the f32 matrix
+    # cores (v_mfma_f32_16x16x4_f32, 157.3 TFLOP/s dense) beside it, with its
+    # own dominant group against that peak.
+    if args.f32_mfma_line and cfg["dtype"] == "f32" and args.f32_math == "split":
+        ctx.set_f32_math(hip.F32_MATH_MFMA_F32)
+        p2, infos2, groups2, per2, peak2, elt2, line = measure_encoder(
+            ctx, args.config, max(5, args.steps // 4), max(2, args.warmup // 2), args.kernel_repeats, "mfma",
+            check=not args.no_check)
+        totals2 = {g: sum(per2[k] for k in ks) for g, ks in groups2.items()}
+        traffic2 = read_traffic(args.config, line["matrix_math"])
+        dominant2 = max(totals2, key=totals2.get)
+        line["roofline"] = roof(p2, infos2, groups2, peak2, elt2, dominant2, "roofline_f32", traffic2)
+        if "flash_attention" in groups2:
+            line["attention"] = roof(p2, infos2, groups2, peak2, elt2, "flash_attention", "attention_f32", traffic2)
+        p2.close()
+        ctx.set_f32_math(hip.F32_MATH_SPLIT_BF16)
+        result["f32_mfma"] = line
+
     # The other configurations: their own µs/block, and their attention
     # against the f16 matrix cores' peak (2.5 PFLOP/s dense).
     others = [c for c in args.other_configs.split(",") if c and c != args.config]
@@ -918,7 +943,8 @@ def main() -> int:
             ctx, name, max(5, args.steps // 4), max(2, args.warmup // 2), args.kernel_repeats, args.f32_math,
             check=not args.no_check and name == "vit-b-518")
         if "flash_attention" in groups2:
-            line["attention"] = roof(p2, infos2, groups2, peak2, elt2, "flash_attention", f"attention_{name}", {})
+            line["attention"] = roof(p2, infos2, groups2, peak2, elt2, "flash_attention", f"attention_{name}",
+                                     read_traffic(name, line["matrix_math"]))
         p2.close()
         result["configs"][name] = line
 
