@@ -1385,8 +1385,38 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 // (148 x 148 x 64 -> 64: 19.8 us against 24.6 with 64 x 64).
                 if (conv && !tile_forced)
                     chosen = gn <= 32 && wgs_of(TILE_128x32) >= ctx->compute_units ? TILE_128x32 : TILE_32x64;
+                // A stride-1 convolution over an image with at least a tile per
+                // CU: the direct kernel, which stages each input window once
+                // for all nine taps (k_conv_direct.inc).
+                if (conv && fmath != Math::F32 && (!tile_forced || chosen == TILE_CONV3) && !getenv("BL_CONV_NO_DIRECT") &&
+                    conv_direct_fits(ga)) {
+                    uint32_t oy_first, trows, tcols, nbs;
+                    conv_direct_tiles(ga, oy_first, trows, tcols, nbs);
+                    uint64_t min_tiles = ctx->compute_units;
+                    if (const char *force = getenv("BL_CONV_DIRECT_MIN_TILES")) min_tiles = (uint64_t)atoll(force);
+                    if ((uint64_t)trows * tcols * nbs >= min_tiles) chosen = TILE_CONV3;
+                    else if (chosen == TILE_CONV3) chosen = TILE_32x64;
+                }
+                if (chosen == TILE_CONV3) {
+                    // Weights resident in LDS when one chunk of 32 input
+                    // channels holds them (the LDS of a per-tile chunk): more
+                    // chunks resident cost a workgroup per CU, which measured
+                    // slower than restaging (148 x 148 x 64 -> 64: 20.4 us
+                    // resident at one per CU, 14.5 restaged at two; 518 x 518
+                    // x 32 -> 32: 35.2 resident, 37.6 restaged). As many
+                    // workgroups per CU as LDS holds (at most 4), persistent
+                    // over the tiles.
+                    const uint32_t chunks = (ga.p2 + CD_CC - 1) / CD_CC;
+                    const char *res = getenv("BL_CONV_DIRECT_RESIDENT");
+                    ga.cd_resident = (res ? atoi(res) != 0 && chunks <= 3 : chunks == 1) ? chunks : 0;
+                    const uint32_t lds = conv_direct_lds(fmath, ga.cd_resident);
+                    const uint32_t per_cu = std::max<uint32_t>(1, std::min<uint32_t>(4, 160 * 1024 / lds));
+                    ga.cd_grid = per_cu * ctx->compute_units;
+                    if (const char *force = getenv("BL_CONV_DIRECT_GRID")) ga.cd_grid = (uint32_t)atoi(force);
+                }
+                if (chosen == TILE_CONV3 && !(conv && fmath != Math::F32 && conv_direct_fits(ga))) chosen = TILE_32x64;
                 ga.ksplit = 1;
-                if (conv && !getenv("BL_CONV_NO_SPLIT_K")) {
+                if (conv && chosen != TILE_CONV3 && !getenv("BL_CONV_NO_SPLIT_K")) {
                     const uint64_t wgs = wgs_of(chosen);
                     const uint32_t steps = ga.k_pad / 32;
                     if (wgs < ctx->compute_units && steps >= 4) {
@@ -1406,8 +1436,11 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 L.gemm = ga;
                 L.tile = chosen;
                 variant = std::string(fmath == Math::F16 ? "mfma-f16" : fmath == Math::F32 ? "mfma-f32" : "mfma-bf16x3") +
-                          " " + std::to_string(gemm_tile_rows(chosen)) + "x" +
-                          std::to_string(gemm_tile_cols(chosen)) + (ga.kslices == 2 ? " bk64" : "") +
+                          (chosen == TILE_CONV3 ? std::string(" direct ") + std::to_string(CD_TH) + "x" + std::to_string(CD_TW) + "x" +
+                                                      std::to_string(CD_NB)
+                                                : " " + std::to_string(gemm_tile_rows(chosen)) + "x" +
+                                                      std::to_string(gemm_tile_cols(chosen))) +
+                          (ga.kslices == 2 ? " bk64" : "") +
                           (ga.kgroups > 1 && !conv ? " k" + std::to_string(ga.kgroups) : std::string()) +
                           (ga.ksplit > 1 ? " splitk" + std::to_string(ga.ksplit) : std::string());
                 break;

@@ -93,6 +93,11 @@ struct GemmArgs {
     float ln_eps;
     // The ring kernel's per-lane epilogue in place of the one through LDS.
     uint32_t lane_epilogue;
+    // The direct 3x3 convolution: workgroups of its persistent grid (each
+    // takes every cd_grid-th tile of its XCD's share), and whether they keep
+    // every input-channel chunk's weights in LDS (staged once) or stage one
+    // chunk's per tile.
+    uint32_t cd_grid, cd_resident;
     // ln_shadow's plane distance in elements (0: m * n).
     uint64_t ln_plane;
     // The class-token prepend fused into this product (a patch embedding,
@@ -272,10 +277,49 @@ hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStrea
 hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
 hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s);
 
+// The direct 3x3 convolution (k_conv_direct.inc): output rows, columns and
+// channels per workgroup, input channels per staged chunk.
+constexpr int CD_TH = 2, CD_TW = 64, CD_NB = 32, CD_CC = 32;
+constexpr int CD_HR = CD_TH + 2, CD_HC = CD_TW + 2;
+constexpr int CD_HALO = CD_HR * CD_HC * 64, CD_WTS = 9 * CD_NB * 64;  // bytes per plane
+
+struct ConvTile {
+    uint32_t oy0, ox0, n0;
+};
+// The part's tiles: the first output row, and tile rows, columns and channel
+// blocks.
+__host__ __device__ inline void conv_direct_tiles(const GemmArgs &a, uint32_t &oy_first, uint32_t &rows,
+                                                  uint32_t &cols, uint32_t &nbs) {
+    const uint32_t W = a.p1;
+    oy_first = a.row0 / W;
+    const uint32_t oy_last = (a.row1 - 1) / W;
+    rows = (oy_last - oy_first + CD_TH) / CD_TH;
+    cols = (W + CD_TW - 1) / CD_TW;
+    nbs = (a.n + CD_NB - 1) / CD_NB;
+}
+// Whether the direct kernel takes this convolution: stride 1 (output the
+// input's size), whole 8-channel groups in and whole 32-channel blocks out,
+// one pass (no split k), A as stored (not split planes), no fold.
+__host__ inline bool conv_direct_fits(const GemmArgs &a) {
+    return a.load == 3 && a.p3 == 1 && a.p4 == a.p1 && a.m == a.p0 * a.p1 && a.p2 % 8 == 0 && a.n % CD_NB == 0 &&
+           a.k == 9 * a.p2 && a.ksplit <= 1 && a.a_planes == 0 && !a.ln_stats && !a.ln_out && !a.flash_ops &&
+           a.row0 < a.row1 && a.row1 <= a.m && (a.epi_mode == 0 || a.epi_mode == 3) && (uint64_t)a.p0 * a.p1 * a.p2 < (1ull << 40);
+}
+
+// Bytes of LDS the kernel holds: the window and `chunks_held` (at least one) chunks
+// of weights, per plane.
+__host__ inline uint32_t conv_direct_lds(Math m, uint32_t chunks_held) {
+    const uint32_t planes = m == Math::SPLIT ? 2 : 1;
+    return planes * (CD_HALO + (chunks_held ? chunks_held : 1) * CD_WTS);
+}
+
 // GEMM tile shapes the dispatcher can pick from: BM x BN.
-enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_128x32 = 4, TILE_64x96 = 5, TILE_COUNT = 6 };
-inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128, 64}; return r[t]; }
-inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64, 32, 96}; return c[t]; }
+// TILE_CONV3: the direct 3x3 convolution (2 output rows x 64 columns x 32
+// channels per workgroup; its rows and columns below are the pixels and
+// channels of one tile).
+enum GemmTile : int { TILE_64x64 = 0, TILE_32x64 = 1, TILE_64x128 = 2, TILE_128x64 = 3, TILE_128x32 = 4, TILE_64x96 = 5, TILE_CONV3 = 6, TILE_COUNT = 7 };
+inline int gemm_tile_rows(int t) { const int r[] = {64, 32, 64, 128, 128, 64, 128}; return r[t]; }
+inline int gemm_tile_cols(int t) { const int c[] = {64, 64, 128, 64, 32, 96, 32}; return c[t]; }
 // K and N of a packed B are padded to these.
 constexpr uint32_t PACK_K = 32, PACK_N = 128;
 

@@ -66,10 +66,11 @@ def test_conv3x3_matches_the_oracle(ctx, h, w, cin, cout, stride, bias):
     assert max_abs_err(got16, want16) <= F16_TOL
 
 
-def test_the_relu_prologue_and_epilogues_of_a_residual_unit(ctx):
+@pytest.mark.parametrize("h,w,c", [(19, 21, 64), (148, 150, 64)])
+def test_the_relu_prologue_and_epilogues_of_a_residual_unit(ctx, h, w, c):
     # x + conv2(relu(conv1(relu(x)))): the outer ReLU a prologue (x is read
-    # twice), the inner an epilogue, the add fused into conv2.
-    h, w, c = 19, 21, 64
+    # twice), the inner an epilogue, the add fused into conv2. At 148 x 150
+    # both convolutions take the direct kernel.
     x = oracle.uniform(21, h * w * c, -2.0, 2.0)
     w1, w2 = oracle.fan_in_weights(22, 9 * c * c, 9 * c), oracle.fan_in_weights(23, 9 * c * c, 9 * c)
     b1, b2 = oracle.uniform(24, c, -0.1, 0.1), oracle.uniform(25, c, -0.1, 0.1)
@@ -81,11 +82,53 @@ def test_the_relu_prologue_and_epilogues_of_a_residual_unit(ctx):
     g = chain(vals, ops)
     names = g.lower(ir.FUSION_ON).names()
     assert names == ["relu-conv2d3x3+relu", "conv2d3x3+add"]
+    assert all((" direct " in lab) == (h > 100) for lab in labels_of(ctx, g)), labels_of(ctx, g)
     first = oracle.conv3x3(oracle.relu(x), w1, b1, h, w, c, c)
     want = oracle.add(oracle.conv3x3(oracle.relu(first), w2, b2, h, w, c, c), x)
     for fusion in (ir.FUSION_ON, ir.FUSION_OFF):
         for parts in (1, 4):
             assert_close(run(ctx, g, vals, parts, fusion=fusion), want, f"residual unit fusion {fusion} parts {parts}")
+
+
+def labels_of(ctx, g, parts=1, dtype=hip.F32, fusion=ir.FUSION_ON):
+    prep = ir.prepare(ctx, g, fusion, parts, True, dtype)
+    labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+    prep.close()
+    return labels
+
+
+# Stride-1 convolutions over images with at least a tile (2 rows x 64 columns
+# x 32 channels) per CU take the direct kernel, which stages each input window
+# in LDS once for the nine taps: the decoder's 148 x 148 x 64 units and
+# fusion convolutions, the head's 296 x 296 x 64 -> 32 and 518 x 518 x 32 ->
+# 32 ones; ragged widths (tile columns past the image), odd tile-row counts,
+# input channels not a whole 32-channel chunk, and parts.
+@pytest.mark.parametrize("h,w,cin,cout,bias", [
+    (148, 148, 64, 64, True),
+    (148, 148, 48, 64, True),
+    (296, 296, 64, 32, True),
+    (201, 130, 40, 32, False),
+    (518, 518, 32, 32, True),
+])
+def test_the_direct_convolution_matches_the_oracle(ctx, h, w, cin, cout, bias):
+    x = oracle.uniform(31, h * w * cin, -2.0, 2.0)
+    wt = oracle.fan_in_weights(32, 9 * cin * cout, 9 * cin)
+    b = oracle.uniform(33, cout, -0.1, 0.1) if bias else None
+    vals = {0: x, 1: wt}
+    if bias:
+        vals[2] = b
+    g = chain(vals, [ir.op(ir.OP_CONV3X3, [0, 1, 2 if bias else ir.NONE], [h, w, cin, cout, 1])])
+    labels = labels_of(ctx, g)
+    assert len(labels) == 1 and " direct " in labels[0], labels
+    want = oracle.conv3x3(x, wt, b, h, w, cin, cout, 1)
+    for parts in (1, 3):
+        assert_close(run(ctx, g, vals, parts), want, f"direct conv3x3 {h}x{w}x{cin}->{cout}, {parts} parts")
+    assert " direct " in labels_of(ctx, g, dtype=hip.F16)[0]
+    got16 = run(ctx, g, vals, 1, hip.F16)
+    want16 = oracle.conv3x3(f16(x), f16(wt), f16(b) if bias else None, h, w, cin, cout, 1)
+    err = max_abs_err(got16, want16)
+    print(f"direct conv3x3 {h}x{w}x{cin}->{cout} f16: max abs error {err:.3e}")
+    assert err <= F16_TOL
 
 
 @pytest.mark.parametrize("h,w,cin,cout,f", [(37, 37, 48, 48, 4), (37, 37, 96, 96, 2), (3, 5, 7, 3, 2), (1, 2, 1, 1, 2)])
