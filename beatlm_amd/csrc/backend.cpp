@@ -1081,6 +1081,7 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     ks->arenas = arenas;
     ks->sets = n_sets;
     uint64_t scratch_bytes = 0;
+    uint64_t flash_counter_bytes = 0;  // the largest in-kernel merge's arrival counters
     std::vector<std::pair<size_t, size_t>> flash_users;  // (kernel, set) whose FlashArgs need scratch
     std::vector<std::pair<size_t, size_t>> split_users;  // (kernel, set) of split-k GEMMs
 
@@ -1525,11 +1526,14 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 L.fl.wgs = fp.wgs;
                 L.fl.units = fp.units;
                 L.fl.merge = fp.merge;
+                L.fl.merge_inline = fp.merge && fp.counters && !getenv("BL_FLASH_MERGE_LAUNCH");
                 scratch_bytes = std::max(scratch_bytes, fp.scratch_bytes);
+                flash_counter_bytes = std::max(flash_counter_bytes, fp.counter_bytes);
                 flash_users.push_back({ki, si});
                 variant = fmath == Math::F32 ? "mfma-f32 splits=" + std::to_string(fp.splits)
                                              : std::string(fmath == Math::F16 ? "mfma-f16" : "mfma-bf16x3") + " 32x32 runs=" +
-                                                   std::to_string(fp.wgs) + (fp.merge ? " merged" : "");
+                                                   std::to_string(fp.wgs) +
+                                                   (L.fl.merge_inline ? " merged in-kernel" : fp.merge ? " merged" : "");
                 break;
             }
             }
@@ -1572,6 +1576,11 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     const uint32_t whole = n ? n - 1 : 0;
     const size_t pack_item = items.size();
     if (pack_total) items.push_back({pack_total, 0, whole, -1, 0});
+    // The attention scratch: the in-kernel merge's arrival counters in front
+    // (every flash kernel's at the same bytes, zero between launches), then
+    // the largest flash kernel's operands and partial results.
+    const uint64_t counter_bytes = align256(flash_counter_bytes);
+    if (scratch_bytes) scratch_bytes = counter_bytes + align256(scratch_bytes);
     const size_t scratch_item = items.size();
     if (scratch_bytes) items.push_back({align256(scratch_bytes), 0, whole, -1, 0});
     // Each split-k GEMM's partial sums: the largest over its binding sets,
@@ -1629,9 +1638,10 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
         // Kernels run one after another on the stream, so every flash kernel
         // uses the same scratch: operands, then partial outputs and statistics.
         for (auto [ki, si] : flash_users)
-            bind_flash_scratch(ks->kernels[ki].per_set[si].fl, ks->kernels[ki].per_set[si].math, ks->scratch);
+            bind_flash_scratch(ks->kernels[ki].per_set[si].fl, ks->kernels[ki].per_set[si].math, ks->scratch, counter_bytes);
         // Zeroed once: the operands' padding keys (past the last token) are
-        // never written by a fused QKV projection and must stay finite.
+        // never written by a fused QKV projection and must stay finite, and the
+        // merge's arrival counters start at zero (each launch leaves them so).
         if (hipMemset(ks->scratch, 0, scratch_bytes) != hipSuccess)
             return bad(BL_ERR_HIP, "clearing %llu bytes of attention scratch", (unsigned long long)scratch_bytes);
         // A flash kernel (f16 or bf16x3) whose qkv comes straight from QKV

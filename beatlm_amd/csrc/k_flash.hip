@@ -7,7 +7,7 @@
 //   qkv  [T][3][H][64]  (queries, keys, values of each token, heads side by side)
 //   out  [T][H * 64]    (heads side by side, as the output projection reads them)
 //
-// Launches per spec:
+// Launches per spec (the prep only when no projection wrote K and Vt):
 //  1. flash_prep_kernel writes the keys as K [H][T_pad][64] and the values
 //     transposed as Vt [H][64][T_pad], once, in the matrix cores' operand type
 //     (f16, f32, or hi and lo bf16 planes), zero-padded to whole 64-key tiles.
@@ -37,11 +37,14 @@
 //     merged inside one XCD and its L2.
 //     A segment that covers all keys of its query tile writes the output; one
 //     that covers part of them writes (max, sum, unnormalised output) to
-//     scratch, and attn_merge_kernel combines them, its workgroups dealt to
-//     the XCDs that computed their tiles. (Merging inside the flash kernel,
-//     each run waiting on its XCD's other runs and reading their results
-//     from the XCD's L2, measured slower than this second launch: 27.0
-//     against 21.8 us at 1370 tokens and 6 heads.)
+//     scratch. The runs that split a tile then combine it themselves at the
+//     end of the kernel: each adds one to the tile's arrival counter once its
+//     partial result is stored (agent-coherent stores), one wave per
+//     workgroup waits until all the tile's runs have arrived, and run j of r
+//     combines rows [256 j / r, 256 (j + 1) / r) (agent-coherent loads). The
+//     grid is one workgroup per CU, all resident at once, so every wait ends;
+//     it is bounded all the same. attn_merge_kernel, a launch of its own,
+//     does the same combination when BL_FLASH_MERGE_LAUNCH is set.
 //  3. flash16_kernel (f32 math, v_mfma_f32_16x16x4_f32): a workgroup owns 64
 //     queries of one head and one range of key tiles (split when there are
 //     too few query tiles to fill the chip); merged by flash16_merge_kernel.
@@ -49,6 +52,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
+#include <vector>
 
 #include "device_common.hpp"
 
@@ -243,6 +247,22 @@ __host__ __device__ inline XcdShare xcd_share(uint32_t pairs, uint32_t kt, uint3
     return sh;
 }
 
+// The pairs (local indices within the XCD's share) of a run's first and last
+// segments, and whether each is split, i.e. the run covers only part of its
+// key tiles. The last is reported only when it differs from the first.
+struct RunSplits {
+    uint32_t first, last;
+    bool first_split, last_split;
+};
+__host__ __device__ inline RunSplits run_splits(uint32_t u_begin, uint32_t u_end, uint32_t kt) {
+    RunSplits r;
+    r.first = u_begin / kt;
+    r.last = (u_end - 1) / kt;
+    r.first_split = u_begin % kt != 0 || u_end < (r.first + 1) * kt;
+    r.last_split = r.last != r.first && u_end % kt != 0;
+    return r;
+}
+
 // Partial results of workgroup g's segments: slot 0 holds its run's first
 // segment, slot 1 its last (segments between them cover whole query tiles and
 // write the output). Row r of a slot: QROWS rows of 64 floats, (max, sum)
@@ -251,15 +271,68 @@ template <Math M> __device__ __forceinline__ uint64_t partial_row(uint32_t g, ui
     return ((uint64_t)g * 2 + slot) * query_rows<M>() + r;
 }
 
+// Partial results that other workgroups of the same launch read (the
+// in-kernel merge) are stored and loaded with the cache policy of agent-scope
+// atomics (sc1: coherent across the device's XCDs and their L2s), so they
+// are visible once the writer's stores have completed, with no L2 write-back
+// between. Buffer descriptors over the partial and statistics arrays give
+// 16- and 8-byte accesses with that policy.
+constexpr int CPOL_AGENT = 16;  // sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, 0x7fffffff, 0x00020000);
+}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x4 coherent_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte, 0, CPOL_AGENT));
+}
+__device__ __forceinline__ f32x2 coherent_load2(__amdgpu_buffer_rsrc_t r, uint32_t byte) {
+    return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, byte, 0, CPOL_AGENT));
+}
+__device__ __forceinline__ void coherent_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte, 0, CPOL_AGENT);
+}
+__device__ __forceinline__ void coherent_store2(__amdgpu_buffer_rsrc_t r, uint32_t byte, f32x2 v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, byte, 0, CPOL_AGENT);
+}
+
+// The in-kernel merge's arrival counter of one pair, one 128-byte line per
+// counter: every run that wrote a partial result of the pair adds 1 once all
+// its waves' stores have completed; every run adds 1 more once it has seen
+// all the runs arrive, and the last of those resets the counter to zero for
+// the next launch. One wave per workgroup polls. Waiting is bounded (a
+// fraction of a second): every workgroup of the grid is resident at once
+// (one per CU, as many as CUs), so the arrivals come unless the device runs
+// fewer workgroups at a time, and then the merge reads what is there instead
+// of waiting for ever.
+constexpr uint32_t COUNTER_STRIDE = 32;  // words
+constexpr uint32_t ARRIVAL_SPIN_LIMIT = 1u << 18;
+__device__ __forceinline__ void arrive_count(uint32_t *ctr) {
+    __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void await_count(const uint32_t *ctr, uint32_t target) {
+    for (uint32_t i = 0; i < ARRIVAL_SPIN_LIMIT; i++) {
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+        __builtin_amdgcn_s_sleep(8);
+    }
+    asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void depart_count(uint32_t *ctr, uint32_t total) {
+    if (__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1)
+        __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Combines rows [r0, r1) of pair `item` (head item / qtiles, query tile
 // item % qtiles) from the partial results of the XCD-local runs vf .. vl that
 // split its key tiles:
 //   O = sum_r 2^(m_r - m) O_r / sum_r 2^(m_r - m) l_r,
-// folded run by run with a running max, MERGE_BATCH runs at a time (every load
-// of a batch issued before the first is used). One invocation per (row, 4
-// columns) at a time out of `nthreads`.
+// folded run by run with a running max, BATCH runs at a time. One invocation
+// per (row, 4 columns) out of `nthreads`, ITEMS of them at a time, every load
+// of an iteration's items and batch issued before the first is used.
+// COHERENT: the partial results were written in this launch (loads with the
+// agent-coherent policy).
 constexpr uint32_t MERGE_BATCH = 8;
-template <Math M>
+template <Math M, bool COHERENT, uint32_t ITEMS, uint32_t BATCH>
 __device__ __forceinline__ void merge_rows(const FlashArgs &a, uint32_t item, uint32_t r0, uint32_t r1, uint32_t tid,
                                            uint32_t nthreads) {
     using T = typename FlashTraits<M>::T;
@@ -272,48 +345,72 @@ __device__ __forceinline__ void merge_rows(const FlashArgs &a, uint32_t item, ui
     const uint32_t head = item / a.qtiles, qt = item % a.qtiles;
     // The first run holds this tile in its second slot unless the run starts with it.
     const uint32_t first_slot = run_begin(vf, sh.U, sh.G) < u0 ? 1 : 0;
-    for (uint32_t w = tid; w < (r1 - r0) * (HD / 4); w += nthreads) {
-        const uint32_t r = r0 + w / (HD / 4), d = (w % (HD / 4)) * 4;
-        const uint32_t q = a.row0 + qt * QROWS + r;
-        if (q >= a.row1) continue;
-        float m = -INFINITY, l = 0.0f;
-        f32x4 acc = {0, 0, 0, 0};
-        for (uint32_t v0 = vf; v0 <= vl; v0 += MERGE_BATCH) {
-            f32x2 st[MERGE_BATCH];
-            f32x4 ov[MERGE_BATCH];
+    const uint32_t n = (r1 - r0) * (HD / 4);
+    for (uint32_t w0 = tid; w0 < n; w0 += ITEMS * nthreads) {
+        float m[ITEMS], l[ITEMS];
+        f32x4 acc[ITEMS];
 #pragma unroll
-            for (uint32_t b = 0; b < MERGE_BATCH; b++) {
-                const uint32_t v = v0 + b;
-                st[b] = f32x2{-INFINITY, 0.0f};
-                ov[b] = f32x4{0, 0, 0, 0};
-                if (v <= vl) {
-                    const uint64_t row = partial_row<M>(v * 8 + x, v == vf ? first_slot : 0, r);
-                    st[b] = *(const f32x2 *)(a.stats + 2 * row);
-                    ov[b] = *(const f32x4 *)(a.partial + row * HD + d);
+        for (uint32_t i = 0; i < ITEMS; i++) {
+            m[i] = -INFINITY;
+            l[i] = 0.0f;
+            acc[i] = f32x4{0, 0, 0, 0};
+        }
+        for (uint32_t v0 = vf; v0 <= vl; v0 += BATCH) {
+            f32x2 st[ITEMS][BATCH];
+            f32x4 ov[ITEMS][BATCH];
+#pragma unroll
+            for (uint32_t i = 0; i < ITEMS; i++) {
+                const uint32_t w = w0 + i * nthreads;
+                const uint32_t r = r0 + w / (HD / 4), d = (w % (HD / 4)) * 4;
+#pragma unroll
+                for (uint32_t b = 0; b < BATCH; b++) {
+                    const uint32_t v = v0 + b;
+                    st[i][b] = f32x2{-INFINITY, 0.0f};
+                    ov[i][b] = f32x4{0, 0, 0, 0};
+                    if (v <= vl && w < n) {
+                        const uint64_t row = partial_row<M>(v * 8 + x, v == vf ? first_slot : 0, r);
+                        if constexpr (COHERENT) {
+                            st[i][b] = coherent_load2(coherent_rsrc(a.stats), (uint32_t)(row * 8));
+                            ov[i][b] = coherent_load4(coherent_rsrc(a.partial), (uint32_t)((row * HD + d) * 4));
+                        } else {
+                            st[i][b] = *(const f32x2 *)(a.stats + 2 * row);
+                            ov[i][b] = *(const f32x4 *)(a.partial + row * HD + d);
+                        }
+                    }
                 }
             }
-            float m_new = m;
 #pragma unroll
-            for (uint32_t b = 0; b < MERGE_BATCH; b++) m_new = fmaxf(m_new, st[b][0]);
-            const float wa = __builtin_amdgcn_exp2f(m - m_new);
-            l *= wa;
-            acc *= wa;
+            for (uint32_t i = 0; i < ITEMS; i++) {
+                float m_new = m[i];
 #pragma unroll
-            for (uint32_t b = 0; b < MERGE_BATCH; b++) {
-                const float wb = __builtin_amdgcn_exp2f(st[b][0] - m_new);  // 0 for a run past vl
-                l += st[b][1] * wb;
-                acc += ov[b] * wb;
+                for (uint32_t b = 0; b < BATCH; b++) m_new = fmaxf(m_new, st[i][b][0]);
+                const float wa = __builtin_amdgcn_exp2f(m[i] - m_new);
+                l[i] *= wa;
+                acc[i] *= wa;
+#pragma unroll
+                for (uint32_t b = 0; b < BATCH; b++) {
+                    const float wb = __builtin_amdgcn_exp2f(st[i][b][0] - m_new);  // 0 for a run past vl
+                    l[i] += st[i][b][1] * wb;
+                    acc[i] += ov[i][b] * wb;
+                }
+                m[i] = m_new;
             }
-            m = m_new;
         }
-        const float inv = 1.0f / l;
-        if constexpr (M == Math::SPLIT) {
-            store_f32x4((float *)a.out, ((uint64_t)q * H + head) * HD + d, acc * inv, a.out_planes);
-        } else {
-            f16x4 w4;
 #pragma unroll
-            for (int e = 0; e < 4; e++) w4[e] = (_Float16)(acc[e] * inv);
-            *(f16x4 *)((T *)a.out + ((uint64_t)q * H + head) * HD + d) = w4;
+        for (uint32_t i = 0; i < ITEMS; i++) {
+            const uint32_t w = w0 + i * nthreads;
+            const uint32_t r = r0 + w / (HD / 4), d = (w % (HD / 4)) * 4;
+            const uint32_t q = a.row0 + qt * QROWS + r;
+            if (w >= n || q >= a.row1) continue;
+            const float inv = 1.0f / l[i];
+            if constexpr (M == Math::SPLIT) {
+                store_f32x4((float *)a.out, ((uint64_t)q * H + head) * HD + d, acc[i] * inv, a.out_planes);
+            } else {
+                f16x4 w4;
+#pragma unroll
+                for (int e = 0; e < 4; e++) w4[e] = (_Float16)(acc[i][e] * inv);
+                *(f16x4 *)((T *)a.out + ((uint64_t)q * H + head) * HD + d) = w4;
+            }
         }
     }
 }
@@ -629,22 +726,58 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
                     }
             } else {
                 const uint64_t row = partial_row<M>(g, first ? 0 : 1, wave * 32 + l32);
-                float *part = args.partial + row * HD;
+                if (args.merge_inline) {
+                    const __amdgpu_buffer_rsrc_t pr = coherent_rsrc(args.partial);
 #pragma unroll
-                for (int db = 0; db < 2; db++)
+                    for (int db = 0; db < 2; db++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        *(f32x4 *)(part + 32 * db + 8 * j + 4 * h) =
-                            f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
-                if (h == 0) *(f32x2 *)(args.stats + 2 * row) = f32x2{m_run, l_tot};
+                        for (int j = 0; j < 4; j++)
+                            coherent_store4(pr, (uint32_t)((row * HD + 32 * db + 8 * j + 4 * h) * 4),
+                                            f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]});
+                    if (h == 0) coherent_store2(coherent_rsrc(args.stats), (uint32_t)(row * 8), f32x2{m_run, l_tot});
+                } else {
+                    float *part = args.partial + row * HD;
+#pragma unroll
+                    for (int db = 0; db < 2; db++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            *(f32x4 *)(part + 32 * db + 8 * j + 4 * h) =
+                                f32x4{o[db][4 * j], o[db][4 * j + 1], o[db][4 * j + 2], o[db][4 * j + 3]};
+                    if (h == 0) *(f32x2 *)(args.stats + 2 * row) = f32x2{m_run, l_tot};
+                }
             }
         }
+        const bool partial = !(k0 == 0 && k1 == kt);
         u += k1 - k0;
         first = false;
         // Every wave is done with the ring before the next segment refills it,
-        // and no store is left outstanding under the next segment's load counts.
+        // and no store is left outstanding under the next segment's load counts
+        // (nor, for a partial result merged in this launch, before its arrival).
         wait_vmcnt<0>();
         __syncthreads();
+        if (partial && args.merge_inline && tid == 0) arrive_count(args.counters + item * COUNTER_STRIDE);
+    }
+
+    // The in-kernel merge: this workgroup's share of each query tile it
+    // computed part of (at most its first and its last segment). Run j of the
+    // r runs vf .. vl that split the tile combines rows [QROWS j / r,
+    // QROWS (j + 1) / r) once all r runs' waves have arrived.
+    if (args.merge_inline && u_begin < u_end) {
+        const RunSplits rs = run_splits(u_begin, u_end, kt);
+        for (uint32_t s = 0; s < 2; s++) {
+            if (!(s == 0 ? rs.first_split : rs.last_split)) continue;
+            const uint32_t local = s == 0 ? rs.first : rs.last;
+            const uint32_t item = run_begin(xg, pairs, 8) + local;
+            const uint32_t u0 = local * kt;
+            const uint32_t vf = run_of(u0, sh.U, sh.G), vl = run_of(u0 + kt - 1, sh.U, sh.G);
+            const uint32_t r = vl - vf + 1, j = v - vf;
+            uint32_t *ctr = args.counters + item * COUNTER_STRIDE;
+            if (wave == 0) await_count(ctr, r);
+            __syncthreads();
+            if (tid == 0) depart_count(ctr, 2 * r);
+            if (r <= 2) merge_rows<M, true, 4, 2>(args, item, QROWS * j / r, QROWS * (j + 1) / r, tid, THREADS32);
+            else merge_rows<M, true, 2, MERGE_BATCH>(args, item, QROWS * j / r, QROWS * (j + 1) / r, tid, THREADS32);
+        }
     }
 }
 
@@ -665,7 +798,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(FlashArgs a) {
     const XcdShare sh = xcd_share(pairs, kt, a.wgs, x);
     const uint32_t u0 = local * kt;
     if (run_of(u0, sh.U, sh.G) == run_of(u0 + kt - 1, sh.U, sh.G)) return;  // written by attn_kernel
-    merge_rows<M>(a, item, r0, r0 + MERGE_ROWS, threadIdx.x, 256);
+    merge_rows<M, false, 1, MERGE_BATCH>(a, item, r0, r0 + MERGE_ROWS, threadIdx.x, 256);
 }
 
 // ---- 3. the 16 x 16 kernel (f32 math) ----
@@ -857,7 +990,7 @@ hipError_t launch_32(const FlashArgs &a, hipStream_t s) {
     }
     hipLaunchKernelGGL(attn_kernel<M>, dim3(a.wgs), dim3(THREADS32), 0, s, a);
     e = hipGetLastError();
-    if (e != hipSuccess || !a.merge) return e;
+    if (e != hipSuccess || !a.merge || a.merge_inline) return e;
     const uint32_t blocks = 8 * ((a.qtiles * a.heads + 7) / 8) * (query_rows<M>() / MERGE_ROWS);
     hipLaunchKernelGGL(attn_merge_kernel<M>, dim3(blocks), dim3(MERGE_ROWS * (HD / 4)), 0, s, a);
     return hipGetLastError();
@@ -930,6 +1063,8 @@ FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uin
         }
         // Two result slots per workgroup: its first and its last segment.
         extra = (uint64_t)p.wgs * 2 * qrows * (HD + 2) * sizeof(float);
+        p.counters = p.merge ? pairs : 0;
+        p.counter_bytes = (uint64_t)p.counters * COUNTER_STRIDE * sizeof(uint32_t);
     }
     p.scratch_bytes = operand_bytes(m, heads, t_pad) + extra;
     return p;
@@ -951,14 +1086,39 @@ int flash_plan_check(uint32_t tokens, uint32_t heads, uint32_t compute_units, bo
             if (e < b) return BL_ERR_KERNEL;
             if (e > b && (run_of(b, sh.U, sh.G) != v || run_of(e - 1, sh.U, sh.G) != v)) return BL_ERR_KERNEL;
         }
+        // The in-kernel merge: the runs vf .. vl of every split pair, and
+        // only they, name the pair among their split segments (each arrives
+        // and waits for r runs), and their row shares cover the tile once.
+        std::vector<uint32_t> named(sh.n, 0);
+        for (uint32_t v = 0; v < sh.G; v++) {
+            const uint32_t b = run_begin(v, sh.U, sh.G), e = run_begin(v + 1, sh.U, sh.G);
+            if (e <= b) continue;
+            const RunSplits rs = run_splits(b, e, kt);
+            for (uint32_t s = 0; s < 2; s++) {
+                if (!(s == 0 ? rs.first_split : rs.last_split)) continue;
+                const uint32_t local = s == 0 ? rs.first : rs.last;
+                const uint32_t vf = run_of(local * kt, sh.U, sh.G), vl = run_of(local * kt + kt - 1, sh.U, sh.G);
+                if (local >= sh.n || v < vf || v > vl || vf == vl) return BL_ERR_KERNEL;
+                named[local]++;
+            }
+        }
+        const uint32_t qrows = f16 ? query_rows<Math::F16>() : query_rows<Math::SPLIT>();
+        for (uint32_t local = 0; local < sh.n; local++) {
+            const uint32_t vf = run_of(local * kt, sh.U, sh.G), vl = run_of(local * kt + kt - 1, sh.U, sh.G);
+            const uint32_t r = vl - vf + 1;
+            if (named[local] != (r > 1 ? r : 0)) return BL_ERR_KERNEL;
+            for (uint32_t j = 0; j < r; j++)
+                if (qrows * j / r > qrows * (j + 1) / r || (j + 1 == r && qrows * (j + 1) / r != qrows)) return BL_ERR_KERNEL;
+        }
     }
     if (units) *units = total;
     return total == p.units ? BL_OK : BL_ERR_KERNEL;
 }
 
-void bind_flash_scratch(FlashArgs &a, Math m, void *base) {
+void bind_flash_scratch(FlashArgs &a, Math m, void *base, uint64_t counter_bytes) {
     const uint64_t ops = operand_bytes(m, a.heads, a.t_pad);
-    char *b = (char *)base;
+    a.counters = (uint32_t *)base;
+    char *b = (char *)base + counter_bytes;
     a.kp = b;
     a.vt = b + ops / 2;
     a.partial = (float *)(b + ops);

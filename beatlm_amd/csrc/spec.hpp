@@ -183,6 +183,11 @@ struct FlashArgs {
     uint32_t merge;       // 1 when some query tile's key tiles span two runs
     uint32_t prepped;     // 1 when the QKV projection already wrote K and Vt
     uint64_t out_planes;  // bf16x3 math: out kept as hi and lo bf16 planes this many elements apart (0: f32)
+    // f16 and bf16x3 math: 1 when the runs that split a query tile combine
+    // its partial results themselves (no merge launch). One arrival counter
+    // per (head, query tile) pair; every counter is zero between launches.
+    uint32_t merge_inline;
+    uint32_t *counters;
 };
 
 // How a flash attention spec is launched: its grid and the scratch it needs
@@ -190,7 +195,13 @@ struct FlashArgs {
 struct FlashPlan {
     uint32_t splits = 1, qtiles = 0, wgs = 0, merge = 0;
     uint64_t units = 0;
+    // Operands, partial results and statistics. The arrival counters of the
+    // in-kernel merge (`counters` words, one per (head, query tile) pair) are
+    // not counted: they sit in a region of their own in front, shared by every
+    // flash kernel of the scratch and zero between launches.
     uint64_t scratch_bytes = 0;
+    uint32_t counters = 0;
+    uint64_t counter_bytes = 0;  // the counters' bytes (each on a line of its own)
     // False when the shape's unit runs would overflow the kernels' 32-bit
     // run arithmetic (units of one XCD times its runs, 2^32 or more): the
     // backend refuses such a kernel.
@@ -271,8 +282,10 @@ hipError_t launch_gather(const GatherArgs &a, Gather g, bool f16, hipStream_t s)
 hipError_t launch_softmax(const SoftmaxArgs &a, bool f16, hipStream_t s);
 hipError_t launch_flash(const FlashArgs &a, Math m, hipStream_t s);
 FlashPlan plan_flash(Math m, uint32_t tokens, uint32_t heads, uint32_t row0, uint32_t row1, uint32_t compute_units);
-// Points a planned FlashArgs at its scratch (plan.scratch_bytes at `base`).
-void bind_flash_scratch(FlashArgs &a, Math m, void *base);
+// Points a planned FlashArgs at its scratch: the counter region of
+// counter_bytes (at least the plan's counter_bytes, zero) at `base`, then
+// plan.scratch_bytes of operands and partial results.
+void bind_flash_scratch(FlashArgs &a, Math m, void *base, uint64_t counter_bytes);
 hipError_t launch_element(const ElementArgs &a, PerElement p, bool f16, hipStream_t s);
 hipError_t launch_spin(uint64_t ticks, uint32_t blocks, hipStream_t s);
 hipError_t launch_dpt(const DptArgs &a, Dpt k, bool f16, hipStream_t s);

@@ -18,10 +18,13 @@
 // device current and restores the caller's current device before returning.
 //
 // Every call on a GPU shares that GPU's array: calls that overlap on one GPU
-// (two streams, two contexts) race. Nothing in the array needs to start at
-// zero: the prep launch writes every K and Vt element the flash kernel reads
-// (padding keys included), and each split key range writes its partial result
-// before the merge reads it, within the same call.
+// (two streams, two contexts) race. The array's first COUNTER_BYTES hold the
+// in-kernel merge's arrival counters (one per (head, query tile) pair, at the
+// same bytes for every shape): they start at zero, as the whole array does
+// when its code object is loaded, and every call leaves them at zero. The
+// rest needs no initial value: the prep launch writes every K and Vt element
+// the flash kernel reads (padding keys included), and each split key range
+// writes its partial result before the merge reads it, within the same call.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -33,6 +36,7 @@
 namespace {
 
 static __device__ __align__(256) char scratch[BL_STATIC_SCRATCH_BYTES];
+constexpr uint64_t COUNTER_BYTES = 1 << 20;  // 8192 (head, query tile) pairs, 128 bytes each
 
 constexpr int MAX_DEVICES = 64;
 void *device_scratch[MAX_DEVICES];
@@ -90,10 +94,14 @@ extern "C" int bl_flash_attention_static(bl_ctx *ctx, const void *qkv, void *out
     if (!plan.fits)
         return fail(ctx, BL_ERR_TOO_LARGE, "flash attention (static): %llu tokens x %llu heads is beyond the kernel's run arithmetic",
                     (unsigned long long)tokens, (unsigned long long)heads);
-    if (plan.scratch_bytes > BL_STATIC_SCRATCH_BYTES)
+    if (plan.counter_bytes > COUNTER_BYTES)
+        return fail(ctx, BL_ERR_TOO_LARGE,
+                    "flash attention (static): this shape has %llu (head, query tile) pairs, the static array holds counters for %llu",
+                    (unsigned long long)plan.counters, (unsigned long long)(COUNTER_BYTES * plan.counters / plan.counter_bytes));
+    if (COUNTER_BYTES + plan.scratch_bytes > BL_STATIC_SCRATCH_BYTES)
         return fail(ctx, BL_ERR_TOO_LARGE,
                     "flash attention (static): this shape needs %llu bytes of scratch, the static array holds %llu",
-                    (unsigned long long)plan.scratch_bytes, (unsigned long long)BL_STATIC_SCRATCH_BYTES);
+                    (unsigned long long)(COUNTER_BYTES + plan.scratch_bytes), (unsigned long long)BL_STATIC_SCRATCH_BYTES);
     const DeviceScope scope(device);
     hipError_t e = scope.status;
     void *base = nullptr;
@@ -114,8 +122,9 @@ extern "C" int bl_flash_attention_static(bl_ctx *ctx, const void *qkv, void *out
     a.wgs = plan.wgs;
     a.units = plan.units;
     a.merge = plan.merge;
+    a.merge_inline = plan.merge && plan.counters;
     a.prepped = 0;  // the prep launch writes K and Vt into the scratch
-    bl::bind_flash_scratch(a, m, base);
+    bl::bind_flash_scratch(a, m, base, COUNTER_BYTES);
     e = bl::launch_flash(a, m, bl_stream_of(ctx));
     return e == hipSuccess ? BL_OK : bl_fail(ctx, BL_ERR_HIP, hipGetErrorString(e));
 }

@@ -347,8 +347,9 @@ uint64_t bl_kernels_workspace_bytes(const bl_kernels *kernels);
 int bl_kernels_fold_read(bl_kernels *kernels, uint32_t fold, uint32_t set, uint32_t what, void *dst, uint64_t bytes);
 /* The GPU kernel launches behind one bl_kernels_encode_range(first, count,
  * set) call, counted as the kernel nodes of the HIP graph that call replays
- * (a folded LayerNorm adds none; a flash attention adds its merge launch when
- * it has one). BL_ERR_INVALID_ARGUMENT when that range has no captured graph
+ * (a folded LayerNorm adds none; a flash attention adds its prep launch when
+ * no projection writes its operands, and a merge launch only under
+ * BL_FLASH_MERGE_LAUNCH). BL_ERR_INVALID_ARGUMENT when that range has no captured graph
  * (graphs off, or the range not yet encoded). A measurement aid with no
  * counterpart in the reference. */
 int bl_kernels_range_launches(bl_kernels *kernels, uint32_t first, uint32_t count, uint32_t set, uint32_t *launches);
@@ -361,7 +362,8 @@ int bl_kernels_range_launches(bl_kernels *kernels, uint32_t first, uint32_t coun
  * qkv [tokens][3][heads][64] (dtype BL_F32, with the context's f32 math, or
  * BL_F16) into out [tokens][heads * 64], scale as the Scale epilogue's, on
  * the context's stream. The caller passes device pointers to both. Its
- * scratch (the K and Vt operands, partial results of split key ranges) is a
+ * scratch (the K and Vt operands, partial results of split key ranges and
+ * the arrival counters of their in-kernel merge, zero between calls) is a
  * static device array of BL_STATIC_SCRATCH_BYTES that the library holds on
  * each GPU it has run this on until the process ends; a shape needing more
  * is refused with BL_ERR_TOO_LARGE and a message. Nothing is allocated, the

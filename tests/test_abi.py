@@ -112,6 +112,19 @@ def test_the_flash_plan_covers_every_unit_once(tokens, heads, dtype):
     assert units.value == want
 
 
+@pytest.mark.parametrize("cus", [8, 80, 256, 304])
+@pytest.mark.parametrize("tokens,heads", [(1, 1), (257, 6), (1370, 6), (1370, 16), (5477, 6), (40_000, 3)])
+def test_the_in_kernel_merge_counts_every_split_tile_s_runs(cus, tokens, heads):
+    """The in-kernel merge of split query tiles: the runs that split a tile,
+    and only they, name it among their first and last segments (so each tile's
+    arrival counter reaches exactly its run count), and their row shares cover
+    the tile's rows once, on CU counts that divide the units unevenly."""
+    lib = hip.lib()
+    units = C.c_uint64()
+    for dtype in (hip.F32, hip.F16):
+        assert lib.bl_flash_plan_check(tokens, heads, cus, dtype, C.byref(units)) == hip.OK, (cus, tokens, heads, dtype)
+
+
 def test_the_flash_plan_refuses_shapes_beyond_its_run_arithmetic():
     lib = hip.lib()
     units = C.c_uint64()

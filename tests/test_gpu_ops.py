@@ -265,3 +265,42 @@ def test_products_with_few_columns_match_the_oracle(ctx, m, k, n, bias):
     v16 = {t: v.astype(np.float16) for t, v in vals.items()}
     want16 = oracle.relu(oracle.matmul(*(v16[t].astype(np.float32) if t in v16 else None for t in (X, W, B)), m, k, n))
     assert max_abs_err(ir.run_on_gpu(ctx, g, v16, dtype=hip.F16)[Y], want16) <= F16_TOL
+
+
+@pytest.mark.parametrize("t,h,f16", [(1370, 6, False), (1370, 12, True), (257, 6, False), (5477, 6, True)])
+def test_flash_attention_merges_split_tiles_in_kernel_launch_after_launch(ctx, monkeypatch, t, h, f16):
+    """The runs that split a query tile's key tiles merge it inside the flash
+    kernel (arrival counters that every launch leaves at zero): six launches
+    in a row give the same bits, and the same bits as the merge launched as a
+    kernel of its own, both within tolerance of the oracle."""
+    dtype = hip.F16 if f16 else hip.F32
+    qkv = oracle.uniform(60 + t, t * 3 * h * 64, -1.0, 1.0)
+    if f16:
+        qkv = qkv.astype(np.float16)
+    g = attention_chain(t, h, 64, qkv)
+    want = oracle.attention(qkv.astype(np.float32), t, h, 64, 0.125)
+
+    def outputs(runs):
+        prep = ir.prepare(ctx, g, dtype=dtype)
+        try:
+            label = prep.kernels.label(0)
+            prep.write(X, qkv)
+            got = []
+            for _ in range(runs):
+                prep.run()
+                ctx.synchronize()
+                got.append(prep.read(Y))
+            return label, got
+        finally:
+            prep.close()
+
+    label, inline = outputs(6)
+    assert "merged in-kernel" in label, label
+    for i, o in enumerate(inline[1:]):
+        assert np.array_equal(o, inline[0]), f"launch {i + 1} differs from launch 0"
+    err = max_abs_err(inline[0], want)
+    assert err <= (F16_TOL if f16 else 1e-4), f"max abs error {err}"
+    monkeypatch.setenv("BL_FLASH_MERGE_LAUNCH", "1")
+    label2, launched = outputs(1)
+    assert "merged" in label2 and "in-kernel" not in label2, label2
+    assert np.array_equal(launched[0], inline[0])
