@@ -397,6 +397,7 @@ struct Pack {
     Source gamma, beta, bias;
     uint64_t vec_offset = 0;
     bool used = false;
+    bool frag = false;  // fragment-major (packed_at): every reader takes B in registers
     bool folded() const { return gamma.ptr != nullptr; }
     bool reads(uint32_t a, uint64_t off, uint64_t bytes) const {
         auto hit = [&](uint32_t ar, uint64_t o, uint64_t sz) { return sz && ar == a && off < o + sz && o < off + bytes; };
@@ -1552,6 +1553,41 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
     // partial sums for its own launch, each folded LayerNorm's statistics and
     // planes from its producer to its consumer.
     auto align256 = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    // B in registers (GemmArgs::breg) for ring-kernel products of 64-column
+    // tiles of at most 64 rows, one group of waves and 64-wide k-steps whose
+    // k is long against their width (the MLP's second product, k = 4 n: at
+    // 1370 tokens 16.1 -> 15.4 us in bf16x3, 21.6 -> 19.5 at ViT-B, 28.3 ->
+    // 27.8 at ViT-L, and at 5477 tokens 22.3 -> 18.0 in f16). The other
+    // encoder products measured slower so (QKV 12.8 -> 15.8 us in bf16x3,
+    // 24.3 -> 27.5 at ViT-L; out-projections +0.2 to +0.8 us; fc1 +0.5 to
+    // +3.9 us), as did rings of 6 and 8 stages for every product. BL_GEMM_BREG=1 takes B in registers wherever it
+    // applies, BL_GEMM_BREG=0 nowhere. A pack goes fragment-major when every
+    // launch that reads it takes B in registers; the others read their B
+    // through the ring.
+    {
+        const char *knob = getenv("BL_GEMM_BREG");
+        const int breg_mode = knob ? atoi(knob) : -1;  // -1: long products only
+        std::vector<int> all(ks->packs.size(), -1);
+        for (Kernel &k : ks->kernels)
+            for (Launch &L : k.per_set) {
+                if (L.pack < 0) continue;
+                const GemmArgs &g = L.gemm;
+                L.gemm.breg = breg_mode != 0 && L.family == Family::GEMM && (L.math == Math::SPLIT || L.math == Math::F16) &&
+                              g.pipeline && g.load == 0 && g.kgroups == 1 && g.kslices == 2 && g.ksplit <= 1 &&
+                              g.k % 64 == 0 && g.k >= 64 && g.k_pad == g.k && (L.tile == TILE_32x64 || L.tile == TILE_64x64) &&
+                              (breg_mode == 1 || (g.k >= 2 * g.n && g.k / 64 >= 12));
+                int &v = all[L.pack];
+                v = v < 0 ? (int)L.gemm.breg : (v && L.gemm.breg);
+            }
+        for (size_t q = 0; q < ks->packs.size(); q++) ks->packs[q].frag = all[q] == 1;
+        for (Kernel &k : ks->kernels) {
+            for (Launch &L : k.per_set) {
+                if (L.pack >= 0 && !ks->packs[L.pack].frag) L.gemm.breg = 0;
+                if (L.gemm.breg) L.gemm.stages = 4;
+            }
+            if (!k.per_set.empty() && k.per_set[0].gemm.breg) k.label += " breg";
+        }
+    }
     for (const Kernel &k : ks->kernels)
         for (const Launch &L : k.per_set)
             if (L.pack >= 0) ks->packs[L.pack].used = true;
@@ -1757,7 +1793,7 @@ static hipError_t refresh_pack(bl_kernels *k, const Launch &L, hipStream_t s) {
     if (!pk.dynamic && !pk.stale) return hipSuccess;
     PackArgs pa{pk.src, (char *)k->pack_buffer + pk.dst_offset, pk.k, pk.n, pk.k_pad, pk.n_pad,
                 pk.gamma.ptr, pk.beta.ptr, pk.bias.ptr,
-                pk.folded() ? (float *)((char *)k->pack_buffer + pk.vec_offset) : nullptr};
+                pk.folded() ? (float *)((char *)k->pack_buffer + pk.vec_offset) : nullptr, pk.frag ? 1u : 0u};
     hipError_t e = launch_pack(pa, pk.math, s);
     if (e == hipSuccess) {
         pk.stale = false;

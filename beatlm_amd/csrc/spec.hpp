@@ -93,6 +93,10 @@ struct GemmArgs {
     float ln_eps;
     // The ring kernel's per-lane epilogue in place of the one through LDS.
     uint32_t lane_epilogue;
+    // The ring kernel with B in registers: B packed fragment-major
+    // (packed_at), each wave loading its columns' fragments straight into
+    // registers STAGES k-steps ahead; A alone goes through the LDS ring.
+    uint32_t breg;
     // The direct 3x3 convolution: workgroups of its persistent grid (each
     // takes every cd_grid-th tile of its XCD's share), and whether they keep
     // every input-channel chunk's weights in LDS (staged once) or stage one
@@ -127,7 +131,19 @@ struct PackArgs {
     // bias[n] (bias may be null).
     const void *gamma, *beta, *bias;
     float *vec;
+    uint32_t frag;  // pack fragment-major (packed_at) for the B-in-registers kernel
 };
+
+// Where element (n, k) of a packed B plane lies. Row layout: [n_pad][k_pad].
+// Fragment-major: 16-column, 32-deep blocks of 512 elements, column block
+// major, each block in the order the 16 x 16 x 32 MFMA's 64 lanes take their
+// B operand (lane = n % 16 + 16 * (k % 32 / 8), 8 consecutive k a lane), so
+// one 16-byte load per lane is one whole 1 KB block.
+__host__ __device__ inline uint64_t packed_at(uint32_t n, uint32_t k, uint32_t k_pad, bool frag) {
+    if (!frag) return (uint64_t)n * k_pad + k;
+    const uint64_t block = (uint64_t)(n / 16) * (k_pad / 32) + k / 32;
+    return block * 512 + ((k % 32) / 8 * 16 + n % 16) * 8 + k % 8;
+}
 
 // A folded LayerNorm's statistics made from x itself (when the fold's
 // producer has not written them since x last changed): x [rows][cols]

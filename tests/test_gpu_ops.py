@@ -304,3 +304,31 @@ def test_flash_attention_merges_split_tiles_in_kernel_launch_after_launch(ctx, m
     label2, launched = outputs(1)
     assert "merged" in label2 and "in-kernel" not in label2, label2
     assert np.array_equal(launched[0], inline[0])
+
+
+@pytest.mark.parametrize("m,k,n,f16,force", [(1370, 1536, 384, False, False), (1370, 3072, 768, True, False),
+                                             (1370, 384, 1152, False, True), (1370, 384, 1536, True, True)])
+def test_matmul_with_b_in_registers_matches_the_oracle(ctx, monkeypatch, m, k, n, f16, force):
+    """Products whose k is long against their width take B straight into
+    registers from a fragment-major pack (the MLP's second product); forced
+    onto wide products too, the result is the oracle's."""
+    if force:
+        monkeypatch.setenv("BL_GEMM_BREG", "1")
+    a = oracle.uniform(70 + k, m * k, -2.0, 2.0)
+    b = oracle.fan_in_weights(71 + k, k * n, k)
+    bias = oracle.uniform(72 + k, n, -0.1, 0.1)
+    if f16:
+        a, b, bias = a.astype(np.float16), b.astype(np.float16), bias.astype(np.float16)
+    g = chain({X: a, W: b, B: bias}, [ir.op(ir.OP_MATMUL, [X, W, B], [m, k, n])])
+    want = oracle.matmul(a.astype(np.float32), b.astype(np.float32), bias.astype(np.float32), m, k, n)
+    dtype = hip.F16 if f16 else hip.F32
+    prep = ir.prepare(ctx, g, dtype=dtype)
+    try:
+        assert "breg" in prep.kernels.label(0), prep.kernels.label(0)
+    finally:
+        prep.close()
+    got = ir.run_on_gpu(ctx, g, {X: a, W: b, B: bias}, dtype=dtype)[Y]
+    if f16:
+        assert max_abs_err(got, want) <= F16_TOL
+    else:
+        assert_close(got, want, f"matmul {m}x{k}x{n} with B in registers")
