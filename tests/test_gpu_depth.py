@@ -188,3 +188,58 @@ def test_four_vit_l_frames_through_four_binding_sets(ctx, blocks):
             print(f"vit-l-518 frame {f}, {blocks} f16 blocks, 1370 tokens x 1024: max abs error {err:.3e}")
             assert err <= 2e-2, f"frame {f}: max abs error {err:.3e} above 2e-2"
     single.close()
+
+
+def encoder_with_every_block_out(cfg):
+    """bench.build_encoder with every block's output kept as an output of the
+    program (readable after the run, never overwritten)."""
+    grid, width, heads, blocks = cfg["grid"], cfg["width"], cfg["heads"], cfg["blocks"]
+    tokens = grid * grid + 1
+    g = ir.Graph()
+    emb = g.vit_embeddings(grid, PATCH, 3, width, 0)
+    x, next_id, block_ids = emb.output, emb.next_id, []
+    for _ in range(blocks):
+        ids = g.vit_block(ir.VitDims(tokens, width, heads, 4 * width, bench.EPS), x, next_id, ir.OUTPUT)
+        block_ids.append(ids)
+        x, next_id = ids.output, ids.next_id
+    return g, emb, block_ids, tokens
+
+
+@pytest.mark.parametrize("name", ["vit-s-1036", "vit-l-518x4", "vit-b-518"])
+def test_every_block_of_the_f16_encoders_at_full_depth_is_within_2e_2_of_the_oracle(ctx, name):
+    """Configs 3, 4 (one frame) and 5 at full depth (12, 24 and 12 f16
+    blocks): every block's output on the GPU against the oracle's block
+    applied to the same input the GPU block read (the GPU's own previous block
+    output, exactly widened; the oracle's embeddings for the first), at the
+    north star's bar for a block, 2e-2. The end-to-end error against the
+    oracle's whole f32 encoder is printed too: f16 storage rounds the
+    residual stream (|x| up to about 10, so half an f16 ulp is up to 4e-3)
+    twice a block, and those roundings add up over the depth."""
+    cfg = dict(bench.CONFIGS[name])
+    g, emb, block_ids, tokens = encoder_with_every_block_out(cfg)
+    vals = bench.synthetic_values(cfg, emb, block_ids, tokens, np.float16, 2024)
+    prep = ir.prepare(ctx, g, dtype=hip.F16)
+    for tid, v in vals.items():
+        prep.write(tid, v)
+    prep.run()
+    ctx.synchronize()
+    outs = [prep.read(ids.output).astype(np.float32) for ids in block_ids]
+    labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+    prep.close()
+    f = {k: np.asarray(v, np.float32) for k, v in vals.items()}
+    grid, width, heads = cfg["grid"], cfg["width"], cfg["heads"]
+    x = oracle.add(oracle.prepend_token(
+        f[emb.cls], oracle.patch_embed(f[emb.image], f[emb.patch_w], f[emb.patch_b], grid, grid, PATCH, 3, width),
+        grid * grid, width), f[emb.pos])
+    worst = 0.0
+    for b, ids in enumerate(block_ids):
+        w = {n: f[getattr(ids, n)] for n in ir.BLOCK_WEIGHTS}
+        want = oracle.vit_block(x, w, tokens, heads, width // heads, 4 * width, bench.EPS, attention_rounded=False)
+        err = max_abs_err(outs[b], want)
+        worst = max(worst, err)
+        assert err <= 2e-2, f"{name} block {b}: max abs error {err:.3e} above 2e-2"
+        x = outs[b]
+    end_to_end = max_abs_err(outs[-1], oracle_encoder(cfg, emb, block_ids, tokens, vals))
+    print(f"{name}: {len(block_ids)} f16 blocks, {sum('folded into' in s for s in labels)} folded LayerNorms; "
+          f"worst block against the oracle from the same input {worst:.3e}; "
+          f"end to end against the oracle's f32 encoder {end_to_end:.3e}")
