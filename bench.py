@@ -154,6 +154,10 @@ def kernel_bytes(info, elt: int) -> float:
         return float(elt * 4 * rows * d[1] * d[2])
     if info.main == hip.MAIN_MATMUL:
         return float(elt * (rows * d[1] + d[1] * d[2] + rows * d[2]))
+    if info.main == hip.MAIN_CONV3X3:
+        # height, width, cin, cout, stride: the image, the 3 x 3 weights and the
+        # part's output pixels (rows) once each.
+        return float(elt * (d[0] * d[1] * d[2] + 9 * d[2] * d[3] + rows * d[3]))
     return 0.0
 
 
@@ -569,11 +573,14 @@ def depth_model_f16_ms(ctx, runs: int, side: int = 518) -> float:
     return round(ms, 3)
 
 
-def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict:
+def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32, brackets: list | None = None) -> dict:
     """The whole model (12-layer encoder, four tapped feature maps, DPT
     decoder) at each of the reference's five image sides: ms per run over
     `runs` back-to-back runs, and at 518 pixels the summed per-launch time of
-    the encoder's and the decoder's kernels and the decoder's kernels by name."""
+    the encoder's and the decoder's kernels and the decoder's kernels by name.
+    The decoder's dominant family is re-timed between marker launches (as the
+    encoder's groups are, appended to `brackets`) for its HBM traffic, read
+    from the committed counter profile of the model."""
     cfg = ir.DepthConfig.small()
     np_dtype = np.float16 if dtype == hip.F16 else np.float32
     out = {"workload": "Depth Anything V2 Small (ViT-S/14 encoder, taps 3/6/9/12, DPT decoder 48/96/192/384 -> "
@@ -629,14 +636,23 @@ def depth_model_runs(ctx, runs: int, repeats: int, dtype: int = hip.F32) -> dict
             for k in dec:
                 fam.setdefault(prep.program.kernel(k).main, []).append(k)
             main = max(fam, key=lambda f: sum(us[k] for k in fam[f]))
-            t = sum(us[k] for k in fam[main])
+            group = {hip.MAIN_CONV3X3: "conv2d3x3"}.get(main, f"main{main}")
+            t = sum(bracketed(ctx, prep, fam[main], repeats))
+            if brackets is not None:
+                brackets.append({"tag": "decoder", "group": group, "kernels": len(fam[main]), "repeats": repeats})
             flops = sum(kernel_flops(prep.program.kernel(k)) for k in fam[main])
+            nbytes = sum(kernel_bytes(prep.program.kernel(k), 2 if dtype == hip.F16 else 4) for k in fam[main])
             peak = PEAK_TFLOPS["f16"] if dtype == hip.F16 else PEAK_TFLOPS["bf16"] / 3.0
             a = flops / t / 1e6
+            math_name = "f16" if dtype == hip.F16 else "bf16x3"
+            hbm = read_traffic("depth-anything-v2-small", math_name).get(("decoder", group))
             out["decoder_roofline"] = {
                 "kernel": {hip.MAIN_CONV3X3: "conv2d3x3 (all fusions)"}.get(main, str(main)), "launches": len(fam[main]),
                 "bound": "mfma", "achieved": round(a, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
-                "frac": round(a / peak, 4), "us": round(t, 1), "algorithmic_flop": int(flops), "traffic": None}
+                "frac": round(a / peak, 4), "us": round(t, 1), "algorithmic_flop": int(flops),
+                "algorithmic_bytes_per_launch": int(nbytes / len(fam[main])),
+                "traffic": int(hbm) if hbm is not None else None,
+                "traffic_unit": "HBM bytes per launch (mean over the family's launches)"}
         prep.close()
     return out
 
@@ -967,7 +983,7 @@ def main() -> int:
         result["frame_loop"] = loop
 
     if args.depth_runs > 0:
-        result["depth_model"] = depth_model_runs(ctx, args.depth_runs, args.kernel_repeats)
+        result["depth_model"] = depth_model_runs(ctx, args.depth_runs, args.kernel_repeats, brackets=brackets)
         result["depth_model"]["f16_ms_per_run_at_518"] = depth_model_f16_ms(ctx, args.depth_runs)
         result["depth_model"]["checkpoint_load"] = checkpoint_load()
         if not args.no_cpu_baseline:
