@@ -303,19 +303,23 @@ __device__ __forceinline__ void coherent_store2(__amdgpu_buffer_rsrc_t r, uint32
 // the next launch. One wave per workgroup polls. Waiting is bounded (a
 // fraction of a second): every workgroup of the grid is resident at once
 // (one per CU, as many as CUs), so the arrivals come unless the device runs
-// fewer workgroups at a time, and then the merge reads what is there instead
-// of waiting for ever.
+// fewer workgroups at a time; a wait that runs out writes NaN for its rows,
+// so that such a result can never pass for a right one, instead of waiting
+// for ever.
 constexpr uint32_t COUNTER_STRIDE = 32;  // words
 constexpr uint32_t ARRIVAL_SPIN_LIMIT = 1u << 18;
 __device__ __forceinline__ void arrive_count(uint32_t *ctr) {
     __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void await_count(const uint32_t *ctr, uint32_t target) {
-    for (uint32_t i = 0; i < ARRIVAL_SPIN_LIMIT; i++) {
-        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
-        __builtin_amdgcn_s_sleep(8);
+// Whether the count reached `target` within the bound.
+__device__ __forceinline__ bool await_count(const uint32_t *ctr, uint32_t target) {
+    bool reached = false;
+    for (uint32_t i = 0; i < ARRIVAL_SPIN_LIMIT && !reached; i++) {
+        reached = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target;
+        if (!reached) __builtin_amdgcn_s_sleep(8);
     }
     asm volatile("" ::: "memory");
+    return reached;
 }
 __device__ __forceinline__ void depart_count(uint32_t *ctr, uint32_t total) {
     if (__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1)
@@ -334,7 +338,7 @@ __device__ __forceinline__ void depart_count(uint32_t *ctr, uint32_t total) {
 constexpr uint32_t MERGE_BATCH = 8;
 template <Math M, bool COHERENT, uint32_t ITEMS, uint32_t BATCH>
 __device__ __forceinline__ void merge_rows(const FlashArgs &a, uint32_t item, uint32_t r0, uint32_t r1, uint32_t tid,
-                                           uint32_t nthreads) {
+                                           uint32_t nthreads, bool poison = false) {
     using T = typename FlashTraits<M>::T;
     constexpr uint32_t QROWS = query_rows<M>();
     const uint32_t kt = a.t_pad / KT, H = a.heads, pairs = a.qtiles * H;
@@ -402,7 +406,7 @@ __device__ __forceinline__ void merge_rows(const FlashArgs &a, uint32_t item, ui
             const uint32_t r = r0 + w / (HD / 4), d = (w % (HD / 4)) * 4;
             const uint32_t q = a.row0 + qt * QROWS + r;
             if (w >= n || q >= a.row1) continue;
-            const float inv = 1.0f / l[i];
+            const float inv = poison ? __builtin_nanf("") : 1.0f / l[i];
             if constexpr (M == Math::SPLIT) {
                 store_f32x4((float *)a.out, ((uint64_t)q * H + head) * HD + d, acc[i] * inv, a.out_planes);
             } else {
@@ -772,11 +776,12 @@ __global__ __launch_bounds__(THREADS32, 2) void attn_kernel(FlashArgs args) {
             const uint32_t vf = run_of(u0, sh.U, sh.G), vl = run_of(u0 + kt - 1, sh.U, sh.G);
             const uint32_t r = vl - vf + 1, j = v - vf;
             uint32_t *ctr = args.counters + item * COUNTER_STRIDE;
-            if (wave == 0) await_count(ctr, r);
-            __syncthreads();
+            bool missed = false;
+            if (wave == 0) missed = !await_count(ctr, r);
+            missed = __syncthreads_or(missed);
             if (tid == 0) depart_count(ctr, 2 * r);
-            if (r <= 2) merge_rows<M, true, 4, 2>(args, item, QROWS * j / r, QROWS * (j + 1) / r, tid, THREADS32);
-            else merge_rows<M, true, 2, MERGE_BATCH>(args, item, QROWS * j / r, QROWS * (j + 1) / r, tid, THREADS32);
+            if (r <= 2) merge_rows<M, true, 4, 2>(args, item, QROWS * j / r, QROWS * (j + 1) / r, tid, THREADS32, missed);
+            else merge_rows<M, true, 2, MERGE_BATCH>(args, item, QROWS * j / r, QROWS * (j + 1) / r, tid, THREADS32, missed);
         }
     }
 }
