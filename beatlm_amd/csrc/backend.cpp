@@ -857,9 +857,11 @@ void plan_folds(bl_kernels *ks, const bl_spec *specs, uint32_t n, const bl_bindi
             const Launch &Ln = ks->kernels[li].per_set[si];
             const Launch &G = ks->kernels[gi].per_set[si];
             // The consumer's prologue takes one quad of invocations per tile row
-            // and whole pairs of 32-column blocks, at most 16 of them.
+            // (in two passes for an f16 tile of 128 rows) and whole pairs of
+            // 32-column blocks, at most 16 of them.
+            const int fold_rows = G.math == Math::F16 ? 128 : 64;
             if (Ln.family != Family::LAYER_NORM || G.family != Family::GEMM || !G.gemm.pipeline || G.gemm.load != 0 ||
-                4 * gemm_tile_rows(G.tile) > 256 || D > 1024 || D % 64 != 0 ||
+                gemm_tile_rows(G.tile) > fold_rows || D > 1024 || D % 64 != 0 ||
                 G.gemm.ksplit > 1 || G.gemm.k != D || G.gemm.m != ls.dims[0] || G.gemm.row0 != 0 || G.gemm.row1 != G.gemm.m) {
                 ok = false;
                 break;
@@ -1349,6 +1351,23 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                         chosen = square_few ? TILE_32x64 : TILE_64x64;
                         if (!square_few)
                             ga.stages = gk / 64 >= 24 ? 4 : gk / 64 >= 12 && wgs_of(TILE_64x64) <= 5ull * ctx->compute_units ? 3 : 2;
+                        // Wide products of 12 to 16 k-steps: 128 x 64 tiles
+                        // in a two-stage ring (half the B bytes per output)
+                        // when they leave no CU idle and their last round of
+                        // two workgroups per CU is not a sliver of a round
+                        // (in-encoder with the LayerNorm folded, µs: ViT-B
+                        // QKV 18.6 -> 14.8, ViT-L fc1 30.6 -> 29.3). Products
+                        // of 528 such tiles (a round and 16: ViT-B fc1, ViT-L
+                        // QKV) measured slower, and those of 6 k-steps gained
+                        // nothing once the fold's prologue took two passes
+                        // (ViT-S 1036 QKV 18.3 -> 18.6; ViT-S fc1 in f16):
+                        // they keep 64 x 64.
+                        const uint64_t t128 = wgs_of(TILE_128x64), slots = 2ull * ctx->compute_units;
+                        if (!square_few && gn >= 1024 && gk >= 768 && gk <= 1024 && t128 >= ctx->compute_units &&
+                            (t128 % slots == 0 || t128 % slots >= slots / 8) && !getenv("BL_GEMM_NO_128")) {
+                            chosen = TILE_128x64;
+                            ga.stages = 2;
+                        }
                     }
                     else chosen = (gn >= 1024 && w64 <= 2ull * ctx->compute_units) ? TILE_64x64 : TILE_32x64;
                     // bf16x3 outputs of whole 96-column tiles, at least 1536

@@ -240,6 +240,29 @@ def test_a_folded_layernorm_in_f16_storage_with_offset_rows(ctx, prepared, offse
     assert err <= 2e-2
 
 
+@pytest.mark.parametrize("offset", [0.0, 30.0])
+def test_an_f16_fold_into_tiles_of_128_rows(ctx, prepared, monkeypatch, offset):
+    """An f16 product of 128 x 64 tiles takes its rows' statistics in two
+    passes of its prologue (rows 0-63, then 64-127, 128 rows against the
+    workgroup's 64 quads); the last tile is partial (1370 = 10 x 128 + 90)."""
+    monkeypatch.setenv("BL_GEMM_TILE", "3@1536")
+    prep = prepared(dtype=hip.F16)
+    labels = [prep.kernels.label(k) for k in range(len(prep.kernels))]
+    assert any("128x64" in lab and "< layernorm" in lab for lab in labels), labels
+    v = values(f16=True)
+    v[X] = (offset + v[X].astype(np.float32) / 2).astype(np.float16)
+    for tid, a in v.items():
+        prep.write(tid, a)
+    prep.run()
+    ctx.synchronize()
+    x1 = prep.read(X1).astype(np.float32)
+    v32 = {k: a.astype(np.float32) for k, a in v.items()}
+    got = prep.read(OUT).astype(np.float32)
+    err = float(np.max(np.abs(got - want_out(x1, v32))))
+    print(f"folded LayerNorm into 128-row f16 tiles, rows at {offset}: max abs error {err:.3e}")
+    assert err <= 2e-2
+
+
 def test_the_folded_kernels_encoded_alone_after_the_host_rewrites_x(ctx, prepared):
     """x rewritten by the host: the producer's statistics are stale, so the
     LayerNorm (encoded alone) or its reader (encoded alone, or in a replayed

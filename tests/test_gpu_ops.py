@@ -314,6 +314,7 @@ def test_matmul_with_b_in_registers_matches_the_oracle(ctx, monkeypatch, m, k, n
     onto wide products too, the result is the oracle's."""
     if force:
         monkeypatch.setenv("BL_GEMM_BREG", "1")
+        monkeypatch.setenv("BL_GEMM_TILE", "0")  # 64 x 64: a wide f16 product would take 128-row tiles
     a = oracle.uniform(70 + k, m * k, -2.0, 2.0)
     b = oracle.fan_in_weights(71 + k, k * n, k)
     bias = oracle.uniform(72 + k, n, -0.1, 0.1)
