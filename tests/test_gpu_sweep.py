@@ -2,7 +2,7 @@
 oracle: rows, depths and widths drawn at random (ragged and whole tiles, few
 and many tiles per CU, the depths and widths at which the tile rules switch
 between 32x64, 64x64, 64x96, 128x64 tiles, split A, B in registers and ring
-depths), in f32 storage (bf16x3) and f16 storage, and flash attention at
+depths), in f32 storage (bf16x3 and f32 matrix math) and f16 storage, and flash attention at
 random token and head counts (split and whole query tiles, runs within and
 across pairs), so that every kernel the planners may pick for a shape is
 checked, not only the encoder's. The shapes are fixed by the seed and named
@@ -52,8 +52,12 @@ ATTENTION_SHAPES = _attention_shapes()
 
 
 @pytest.mark.parametrize("m,k,n", MATMUL_SHAPES, ids=[f"{m}x{k}x{n}" for m, k, n in MATMUL_SHAPES])
-@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
-def test_a_product_at_a_random_shape_matches_the_oracle(ctx, m, k, n, f16):
+@pytest.mark.parametrize("math", ["bf16x3", "f32", "f16"])
+def test_a_product_at_a_random_shape_matches_the_oracle(ctx, m, k, n, math):
+    """f32 storage in bf16x3 and in f32 matrix math, and f16 storage."""
+    f16 = math == "f16"
+    if math == "f32":
+        ctx.set_f32_math(hip.F32_MATH_MFMA_F32)
     a = oracle.uniform(m + 7 * k, m * k, -2.0, 2.0)
     b = oracle.fan_in_weights(n + 3 * k, k * n, k)
     bias = oracle.uniform(n + 11, n, -0.1, 0.1)
@@ -61,22 +65,25 @@ def test_a_product_at_a_random_shape_matches_the_oracle(ctx, m, k, n, f16):
         a, b, bias = a.astype(np.float16), b.astype(np.float16), bias.astype(np.float16)
     g = chain({X: a, W: b, B: bias}, [ir.op(ir.OP_MATMUL, [X, W, B], [m, k, n])])
     want = oracle.matmul(a.astype(np.float32), b.astype(np.float32), bias.astype(np.float32), m, k, n)
-    prep = ir.prepare(ctx, g, dtype=hip.F16 if f16 else hip.F32)
     try:
-        label = prep.kernels.label(0)
-        for tid, v in {X: a, W: b, B: bias}.items():
-            prep.write(tid, v)
-        prep.run()
-        ctx.synchronize()
-        got = prep.read(Y).astype(np.float32)
+        prep = ir.prepare(ctx, g, dtype=hip.F16 if f16 else hip.F32)
+        try:
+            label = prep.kernels.label(0)
+            for tid, v in {X: a, W: b, B: bias}.items():
+                prep.write(tid, v)
+            prep.run()
+            ctx.synchronize()
+            got = prep.read(Y).astype(np.float32)
+        finally:
+            prep.close()
     finally:
-        prep.close()
+        ctx.set_f32_math(hip.F32_MATH_SPLIT_BF16)
     if f16:
         err = max_abs_err(got, want)
         assert err <= F16_TOL, f"{m}x{k}x{n} f16 ({label}): max abs error {err:.3e}"
     else:
         bad = oracle.first_mismatch(got, want)
-        assert bad is None, f"{m}x{k}x{n} ({label}): element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
+        assert bad is None, f"{m}x{k}x{n} {math} ({label}): element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
 
 
 def attention_graph(t, h, d):
