@@ -5,8 +5,9 @@ between 32x64, 64x64, 64x96, 128x64 tiles, split A, B in registers and ring
 depths), in f32 storage (bf16x3 and f32 matrix math) and f16 storage, and flash attention at
 random token and head counts (split and whole query tiles, runs within and
 across pairs), so that every kernel the planners may pick for a shape is
-checked, not only the encoder's. The shapes are fixed by the seed and named
-in each case's id.
+checked, not only the encoder's; and the DPT head's 3x3 convolution at random
+image sizes, channel counts and strides. The shapes are fixed by the seed and
+named in each case's id.
 
 Tolerance for f32 storage: |got - want| <= 1e-4 + 1e-4 |want|
 (reference.rs:22-24); for f16 storage, max abs error <= 2e-2 against the
@@ -42,12 +43,26 @@ def _matmul_shapes():
                      (700, 384, 1536), (1370, 4096, 1024), (333, 1024, 1056)]
 
 
+def _conv_shapes():
+    rng = np.random.default_rng(20262)
+    shapes = []
+    while len(shapes) < 14:
+        h, w = int(rng.integers(1, 320)), int(rng.integers(1, 320))
+        cin = int(rng.choice([3, 8, 16, 32, 48, 64, 96, 192, 384]))
+        cout = int(rng.choice([1, 4, 16, 20, 32, 64, 256]))
+        stride = int(rng.choice([1, 1, 2]))
+        if h * w * cin * cout * 9 <= 2_000_000_000:
+            shapes.append((h, w, cin, cout, stride))
+    return shapes
+
+
 def _attention_shapes():
     rng = np.random.default_rng(20261)
     return [(int(rng.integers(1, 2600)), int(rng.integers(1, 17))) for _ in range(10)]
 
 
 MATMUL_SHAPES = _matmul_shapes()
+CONV_SHAPES = _conv_shapes()
 ATTENTION_SHAPES = _attention_shapes()
 
 
@@ -84,6 +99,29 @@ def test_a_product_at_a_random_shape_matches_the_oracle(ctx, m, k, n, math):
     else:
         bad = oracle.first_mismatch(got, want)
         assert bad is None, f"{m}x{k}x{n} {math} ({label}): element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
+
+
+@pytest.mark.parametrize("h,w,cin,cout,stride", CONV_SHAPES, ids=[f"{h}x{w}x{ci}to{co}s{st}" for h, w, ci, co, st in CONV_SHAPES])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+def test_a_convolution_at_a_random_shape_matches_the_oracle(ctx, h, w, cin, cout, stride, f16):
+    """The DPT head's 3x3 convolution (direct, implicit GEMM with or without
+    split k, 128 x 32 tiles, the element-wise gather for narrow channels, as
+    the planner picks for the shape), with bias."""
+    x = oracle.uniform(h + w + cin, h * w * cin, -2.0, 2.0)
+    wt = oracle.fan_in_weights(cout + 5 * cin, 9 * cin * cout, 9 * cin)
+    b = oracle.uniform(cout + 17, cout, -0.1, 0.1)
+    if f16:
+        x, wt, b = x.astype(np.float16), wt.astype(np.float16), b.astype(np.float16)
+    vals = {0: x, 1: wt, 2: b}
+    g = chain(vals, [ir.op(ir.OP_CONV3X3, [0, 1, 2], [h, w, cin, cout, stride])])
+    want = oracle.conv3x3(x.astype(np.float32), wt.astype(np.float32), b.astype(np.float32), h, w, cin, cout, stride)
+    got = ir.run_on_gpu(ctx, g, vals, dtype=hip.F16 if f16 else hip.F32)[Y].astype(np.float32)
+    if f16:
+        err = max_abs_err(got, want)
+        assert err <= F16_TOL, f"conv {h}x{w}x{cin}->{cout} s{stride} f16: max abs error {err:.3e}"
+    else:
+        bad = oracle.first_mismatch(got, want)
+        assert bad is None, f"conv {h}x{w}x{cin}->{cout} s{stride}: element {bad[0]} is {bad[1]}, the oracle says {bad[2]}"
 
 
 def attention_graph(t, h, d):
