@@ -353,8 +353,11 @@ struct Launch {
     // The output's bytes (what the launch writes, the scratch aside).
     const char *out_lo = nullptr, *out_hi = nullptr;
     // A flash kernel whose QKV projections write its K and Vt (fl.prepped):
-    // those projection kernels (one per part).
+    // those projection kernels (one per part). kv_rerun: they store qkv's
+    // queries alone, so the flash kernel cannot make K and Vt from qkv and
+    // runs them again when the scratch does not hold its operands.
     std::vector<uint32_t> kv_producers;
+    bool kv_rerun = false;
     // A LayerNorm folded into the product that reads it (fold >= 0): the
     // LayerNorm itself launches nothing, the product applies it (FOLD_CONSUMER),
     // and the product that wrote its input leaves the input's statistics
@@ -593,6 +596,7 @@ struct FoldState {
 struct RangeGraph {
     uint32_t first, count, set;
     hipGraphExec_t exec;
+    KvState entry;  // what the scratch held when the range was captured
     KvState kv;
     FoldState folds;  // the entries the range sets (touched) and their values after it
     uint32_t launches;  // kernel nodes of the captured graph
@@ -1730,6 +1734,43 @@ extern "C" int bl_kernels_create_internal(bl_ctx *ctx, bl_arenas *arenas, const 
                 F.kv_producers.assign(producers.begin(), producers.end());
                 std::sort(F.kv_producers.begin(), F.kv_producers.end());
             }
+            // A qkv the host never touches, written by nothing but those
+            // projections and read by nothing but these flash kernels, from
+            // an x the host never touches either: the projections store its
+            // queries alone (the flash kernels read K and Vt from the
+            // operands), and a flash kernel whose operands the scratch does
+            // not hold runs its projections again, from the same x, instead of
+            // its own prep (ViT-S/14 518: QKV 11.9 -> 11.3 us).
+            std::vector<uint32_t> ids(internal, internal + n_internal);
+            std::sort(ids.begin(), ids.end());
+            auto is_internal = [&](uint32_t t) { return std::binary_search(ids.begin(), ids.end(), t); };
+            for (auto [ki, si] : flash_users) {
+                Launch &F = ks->kernels[ki].per_set[si];
+                if (!F.fl.prepped || F.kv_producers.empty() || getenv("BL_QKV_WHOLE")) continue;
+                const bl_spec &fsp = specs[ki];
+                const uint32_t t = fsp.bindings[fsp.reads[0]].tensor;
+                bool ok = is_internal(t);
+                for (uint32_t kj = 0; kj < n && ok; kj++) {
+                    const bl_spec &s = specs[kj];
+                    const uint32_t last = s.n_bindings - 1;
+                    const bool writer = s.bindings[last].tensor == t;
+                    bool reader = false;
+                    for (uint32_t b = 0; b < last; b++) reader = reader || s.bindings[b].tensor == t;
+                    if (writer && reader) ok = false;
+                    if (writer) ok = ok && is_internal(s.bindings[s.reads[0]].tensor);
+                    for (uint32_t sj = 0; sj < ks->sets && ok && (writer || reader); sj++) {
+                        const Launch &L = ks->kernels[kj].per_set[sj];
+                        ok = writer ? L.family == Family::GEMM && L.gemm.flash_ops != 0
+                                    : L.family == Family::FLASH && L.fl.prepped && !L.kv_producers.empty();
+                    }
+                }
+                if (!ok) continue;
+                F.kv_rerun = true;
+                for (uint32_t j : F.kv_producers) {
+                    ks->kernels[j].per_set[si].gemm.flash_ops = 2;
+                    if (si == 0) ks->kernels[j].label += " > queries only";
+                }
+            }
         }
     }
     if (n_internal && !getenv("BL_NO_SPLIT_ACTIVATIONS")) keep_split_activations(ks, specs, n, internal, n_internal);
@@ -1844,17 +1885,20 @@ static hipError_t launch(const Launch &L, hipStream_t s) {
 // write (fl.prepped) reads them from the scratch; when the scratch does not
 // hold them (the flash kernel encoded alone, qkv written since by the host
 // or another kernel, or another flash kernel's operands in between) it runs
-// its own prep instead, which makes them from all of qkv.
+// its own prep instead, which makes them from all of qkv (a kv_rerun flash
+// kernel has its projections run again first: run_one).
+static bool kv_held(const Launch &L, const KvState &kv) {
+    if (kv.qkv != L.fl.qkv) return false;
+    if (kv.whole) return true;
+    for (uint32_t p : L.kv_producers)
+        if (std::find(kv.done.begin(), kv.done.end(), p) == kv.done.end()) return false;
+    return true;
+}
+
 static Launch with_kv(const Launch &L, uint32_t i, KvState &kv) {
     Launch run = L;
     if (L.family == Family::FLASH && L.fl.prepped) {
-        bool held = kv.qkv == L.fl.qkv && kv.whole;
-        if (kv.qkv == L.fl.qkv && !kv.whole) {
-            held = true;
-            for (uint32_t p : L.kv_producers)
-                if (std::find(kv.done.begin(), kv.done.end(), p) == kv.done.end()) held = false;
-        }
-        if (!held) {
+        if (!kv_held(L, kv)) {
             run.fl.prepped = 0;
             kv = KvState{};
             kv.qkv = L.fl.qkv;
@@ -1910,6 +1954,16 @@ static hipError_t run_one(bl_kernels *k, uint32_t i, uint32_t set, hipStream_t s
         }
         if (L.fold_role == FOLD_LAYER_NORM) return hipSuccess;
     }
+    if (L.family == Family::FLASH && L.fl.prepped && L.kv_rerun && !kv_held(L, kv)) {
+        // qkv holds the queries alone: its projections make K and Vt again,
+        // from the x they read before (nothing but they write qkv, and the
+        // host touches neither).
+        for (uint32_t p : L.kv_producers) {
+            const hipError_t e = run_one(k, p, set, s, kv, fs);
+            if (e != hipSuccess) return e;
+        }
+        if (!kv_held(L, kv)) return hipErrorInvalidValue;
+    }
     const hipError_t e = launch(with_kv(L, i, kv), s);
     if (e != hipSuccess) return e;
     for (size_t f = 0; f < k->folds.size(); f++) {
@@ -1946,15 +2000,34 @@ extern "C" int bl_kernels_encode(bl_kernels *k, uint32_t kernel, uint32_t set, b
     return BL_OK;
 }
 
+// What a replay of the range may take the attention scratch to hold when it
+// starts: the operands of the range's first flash kernel whose projections
+// all precede the range and store qkv's queries alone, when the scratch now
+// holds them (else a capture would run those projections again); nothing
+// otherwise, so that the graph is right whatever ran before it.
+static KvState range_entry(const bl_kernels *k, uint32_t first, uint32_t count, uint32_t set) {
+    for (uint32_t i = first; i < first + count; i++) {
+        const Launch &L = k->kernels[i].per_set[set];
+        if (L.family != Family::FLASH) continue;
+        if (!L.kv_rerun || L.kv_producers.empty() || L.kv_producers.back() >= first || !kv_held(L, k->kv)) break;
+        return k->kv;
+    }
+    return KvState{};
+}
+
+static bool same_kv(const KvState &a, const KvState &b) {
+    return a.qkv == b.qkv && a.lo == b.lo && a.hi == b.hi && a.whole == b.whole && a.done == b.done;
+}
+
 // The range's launches captured on the context's stream, or null when the
 // capture failed (the caller then launches one by one). The attention
-// scratch is taken to hold nothing when a replay starts, so the graph is
-// right whatever ran before it; `kv` is what it holds after a replay.
-static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, KvState &kv,
-                                     FoldState &fs, uint32_t &launches) {
+// scratch is taken to hold `entry` when a replay starts (the caller replays
+// the graph only then); `kv` is what it holds after a replay.
+static hipGraphExec_t capture_range(bl_kernels *k, uint32_t first, uint32_t count, uint32_t set, const KvState &entry,
+                                     KvState &kv, FoldState &fs, uint32_t &launches) {
     launches = 0;
     hipStream_t s = k->ctx->stream;
-    kv = KvState{};
+    kv = entry;
     // Likewise no fold's statistics are taken as valid when a replay starts.
     fs.valid.assign(k->fold_state.valid.size(), 0);
     fs.touched.assign(k->fold_state.valid.size(), 0);
@@ -1995,16 +2068,17 @@ extern "C" int bl_kernels_encode_range(bl_kernels *k, uint32_t first, uint32_t c
             hipError_t e = L.pack >= 0 ? refresh_pack(k, L, s) : hipSuccess;
             if (e != hipSuccess) return hip_fail(k->ctx, e, k->kernels[i].label.c_str());
         }
+        const KvState entry = range_entry(k, first, count, set);
         const RangeGraph *found = nullptr;
         for (const RangeGraph &g : k->graphs)
-            if (g.first == first && g.count == count && g.set == set) found = &g;
+            if (g.first == first && g.count == count && g.set == set && same_kv(g.entry, entry)) found = &g;
         if (!found) {
             KvState after;
             FoldState folds_after;
             uint32_t launches = 0;
-            hipGraphExec_t exec = capture_range(k, first, count, set, after, folds_after, launches);
+            hipGraphExec_t exec = capture_range(k, first, count, set, entry, after, folds_after, launches);
             if (exec) {
-                k->graphs.push_back({first, count, set, exec, after, folds_after, launches});
+                k->graphs.push_back({first, count, set, exec, entry, after, folds_after, launches});
                 found = &k->graphs.back();
             } else {
                 k->graphs_ok = false;

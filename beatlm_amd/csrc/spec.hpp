@@ -62,7 +62,8 @@ struct GemmArgs {
     EpilogueArgs epi;
     // The QKV projection of a flash attention kernel also writes that
     // kernel's K [planes][H][t_pad][64] and Vt [planes][H][64][t_pad]
-    // operands (its prep step, fused) when flash_ops is set.
+    // operands (its prep step, fused) when flash_ops is set; with 2, qkv
+    // itself receives the queries alone (its first third of columns).
     int flash_ops;
     void *fl_kp, *fl_vt;
     uint32_t fl_tpad;
