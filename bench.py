@@ -236,7 +236,11 @@ def pmc_summary(directory: str) -> str:
     pass's brackets). Each counter is scaled by what it reads for the copy
     (bytes moved / counter KiB). The dispatches between the bench's marker
     launches (spin_kernel) are the bracketed group's: (repeats + 1) launches of
-    each of its kernels."""
+    each of its kernels, and any set-up launches the first of them needs (a
+    flash kernel whose projections store the queries alone runs them again,
+    with their LayerNorm statistics, when another block's operands are in the
+    scratch): kernels launched a number of times that is not a multiple of
+    repeats + 1 are those, listed but not counted."""
     import csv
 
     def rows(name):
@@ -268,15 +272,18 @@ def pmc_summary(directory: str) -> str:
         marks = [i for i, r in enumerate(rs) if "spin_kernel" in r["Kernel_Name"]]
         spans = [rs[marks[2 * j] + 1: marks[2 * j + 1]] for j in range(len(marks) // 2)]
         for b, span in zip(bench["brackets"], spans):
-            kib = sum(float(r["Counter_Value"]) for r in span)
-            per.setdefault((b["tag"], b["group"]), {})[c] = (kib, len(span), b)
             by_kernel = {}
             for r in span:
-                name = r["Kernel_Name"].split("(bl::")[0].replace("void bl::(anonymous namespace)::", "")
-                by_kernel.setdefault(name, []).append(float(r["Counter_Value"]))
+                by_kernel.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+            own = {n for n, v in by_kernel.items() if len(v) % (b["repeats"] + 1) == 0}
+            if sum(len(by_kernel[n]) for n in own) != (b["repeats"] + 1) * b["kernels"]:
+                own = set(by_kernel)
+            kib = sum(sum(by_kernel[n]) for n in own)
+            per.setdefault((b["tag"], b["group"]), {})[c] = (kib, len(span), b)
             for name, v in by_kernel.items():
-                out.append(f"# {b['tag']:10s} {c:10s} {name:48s} dispatches {len(v):4d}  "
-                           f"mean {sum(v) / len(v):12.1f} KiB")
+                short = name.split("(bl::")[0].replace("void bl::(anonymous namespace)::", "")
+                out.append(f"# {b['tag']:10s} {c:10s} {short:48s} dispatches {len(v):4d}  "
+                           f"mean {sum(v) / len(v):12.1f} KiB" + ("" if name in own else "  (set-up, not counted)"))
     for (tag, group), cs in per.items():
         if len(cs) < 2:
             continue  # bracketed in one pass only
