@@ -290,7 +290,12 @@ const char *bl_kernels_label(const bl_kernels *kernels, uint32_t kernel);
  * projection's epilogue wrote into the backend's scratch reads them from
  * there only when nothing has written qkv since; otherwise (the kernel
  * encoded alone, a host write, another kernel over those bytes) it makes
- * them from qkv itself first. Kernels of bl_kernels_create_internal whose work
+ * them from qkv itself first. Under bl_kernels_create_internal, a qkv that is
+ * internal, written by nothing but its projections from an internal x and
+ * read by nothing but flash kernels holds the queries alone (the label of each
+ * projection ends in " > queries only"): such a flash kernel runs its
+ * projections again instead, from x as it is, which in program order is the
+ * x they read before. Kernels of bl_kernels_create_internal whose work
  * another kernel does launch nothing: a LayerNorm folded into the product
  * that reads it, and a class-token prepend fused into the patch embedding
  * before it (which writes the prepend's output; the internal patches tensor
